@@ -1,0 +1,186 @@
+/*
+ * qmoe_capi.h -- C ABI of libqmoe.so, the MI355X (gfx950) kernels for the
+ * Qwen3-30B-A3B decoder-layer hot path: residual RMSNorm, router top-k,
+ * expert dispatch (histogram / scan / permute), the grouped SwiGLU expert
+ * GEMM (MFMA, prefill) and GEMV (decode), the weighted combine, the QKV
+ * projection with per-head RMSNorm + RoPE epilogue, and causal GQA attention
+ * over a contiguous KV cache.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are caller-owned device pointers; outputs and
+ *     workspaces are allocated by the caller.  No entry point allocates,
+ *     frees or synchronises the host.
+ *   - bf16 values are passed as qmoe_bf16 (the raw 16-bit pattern).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream),
+ *     so every call can be captured into a HIP graph.
+ *   - Return 0 on success; QMOE_ERR_INVALID when an argument is rejected
+ *     before anything is launched; QMOE_ERR_HIP when the HIP runtime reports
+ *     an error.  qmoe_last_error() then describes the failure (thread-local).
+ *
+ * Each declaration names the reference interface (charleshong3/nki-moe-7013)
+ * whose behaviour it replaces.
+ */
+#ifndef QMOE_CAPI_H
+#define QMOE_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t qmoe_bf16;
+typedef void* qmoe_stream_t;
+
+#define QMOE_OK 0
+#define QMOE_ERR_INVALID 1
+#define QMOE_ERR_HIP 2
+
+/* GEMM epilogue modes for qmoe_gemm. */
+#define QMOE_GEMM_STORE_BF16 0 /* C[bf16] = A.B^T            */
+#define QMOE_GEMM_STORE_F32 1  /* C[f32]  = A.B^T            */
+#define QMOE_GEMM_ADD_F32 2    /* C[f32] += A.B^T (residual) */
+
+/* Packing granularity of the fused gate/up weight: packed rows
+ * [64j, 64j+32) are gate rows [32j, 32j+32), the next 32 the matching up rows. */
+#define QMOE_W13_GROUP 32
+
+int qmoe_version(void);
+const char* qmoe_last_error(void);
+
+/* Residual RMSNorm.  h = x (+ delta); y = bf16(w * h * rsqrt(mean(h^2) + eps)).
+ *   x, delta, h_out: f32 [rows, H] (delta and h_out may be NULL; h_out may alias x)
+ *   w: bf16 [H]; y_out: bf16 [rows, H]
+ * Replaces: the decoder layer's input/post-attention RMSNorm and residual add,
+ *   NeuronQwen3MoeDecoderLayer.forward qwen_with_nki.py:10179-10207 with
+ *   CustomRMSNorm (fp32 upcast -> normalise -> x weight -> cast) restated at
+ *   qwen_with_nki.py:1372-1384; _nki_rmsnorm_kernel 1286-1342. */
+int qmoe_rmsnorm_residual(const float* x, const float* delta, const qmoe_bf16* w,
+                          int64_t rows, int64_t H, float eps, float* h_out,
+                          qmoe_bf16* y_out, qmoe_stream_t stream);
+
+/* Router: logits = x . w_router^T (+ bias) in fp32; softmax over E; top-k;
+ * renormalise the k weights to sum 1.  Ties pick the lower expert index.
+ *   x: bf16 [T, H]; w_router: bf16 [E, H]; bias: f32 [E] or NULL
+ *   topk_idx: i32 [T, k] (descending weight); topk_w: f32 [T, k];
+ *   logits: f32 [T, E] or NULL.   Limits: E <= 256, k <= 16, H % 8 == 0.
+ * Replaces: NxDI RouterTopK invoked as mlp.router(normed_hidden)
+ *   qwen_with_nki.py:8589-8590 with router dtype fp32 / softmax 9886-9888 and
+ *   normalize_top_k_affinities 9894, 2399-2405. */
+int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias,
+                     int64_t T, int64_t H, int64_t E, int64_t k, int32_t* topk_idx,
+                     float* topk_w, float* logits, qmoe_stream_t stream);
+
+/* Expert dispatch metadata (histogram, exclusive scan, stable permutation).
+ *   topk_idx: i32 [T, k]
+ *   counts: i32 [E]; offsets: i32 [E+1]; slot_token: i32 [T*k] (token of each
+ *   expert-sorted slot, stable by token); token_slot: i32 [T*k] (slot of pair
+ *   t*k+j); active: i32 [E] (experts with rows, ascending);
+ *   tiles: i32 [max_tiles, 4] = (expert, slot_begin, slot_end, 0) in chunks of
+ *   tile_m rows; meta: i32 [4] = (n_tiles, n_active, 0, 0).
+ *   max_tiles must be >= ceil(T*k / tile_m) + E.
+ * Replaces: the block metadata ExpertMLPsV2 builds for
+ *   torch_blockwise_matmul_inference (token_position_to_id / block_to_expert,
+ *   qwen_with_nki.py:5872-5881, 5478-5479; dedup 5656-5667 made unnecessary). */
+int qmoe_moe_permute(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E,
+                     int64_t tile_m, int64_t max_tiles, int32_t* counts, int32_t* offsets,
+                     int32_t* slot_token, int32_t* token_slot, int32_t* active,
+                     int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
+
+/* Decode expert MLPs (bandwidth-bound GEMV form; each touched expert's weights
+ * are streamed once for all tokens routed to it).
+ *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed (QMOE_W13_GROUP);
+ *   w2: bf16 [E, H, I]; offsets/slot_token/active/meta from qmoe_moe_permute;
+ *   act: f32 [T*k, I] workspace; y_slot: f32 [T*k, H] unweighted expert outputs.
+ *   Limits: T*k <= 512 per expert pass, H % 512 == 0, I % 64 == 0.
+ * Replaces: ExpertMLPsV2.forward_selective_loading (decode), restated at
+ *   qwen_with_nki.py:3456-3478; _nki_batched_moe_kernel 1847-1982. */
+int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_bf16* w2,
+                          const int32_t* offsets, const int32_t* slot_token,
+                          const int32_t* active, const int32_t* meta, int64_t T, int64_t H,
+                          int64_t I, int64_t E, int64_t k, float* act, float* y_slot,
+                          qmoe_stream_t stream);
+
+/* Prefill expert MLPs as two grouped GEMMs on bf16 MFMA:
+ *   act[s]    = bf16(silu(x[tok(s)] . Wg[e]^T) * (x[tok(s)] . Wu[e]^T))
+ *   y_slot[s] = bf16(act[s] . W2[e]^T)
+ *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed; w2: bf16 [E, H, I];
+ *   slot_token/tiles/meta from qmoe_moe_permute with tile_m == 128;
+ *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
+ *   Limits: H % 128 == 0, I % 64 == 0, 2I % 128 == 0.
+ * Replaces: _nki_cte_moe_left_gate_up_kernel qwen_with_nki.py:5341-5369 (left)
+ *   and _nki_cte_moe_down_scatter_kernel 4967-5040 (right), dispatched by
+ *   _patched_torch_blockwise_matmul_inference 5872-6003. */
+int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_bf16* w2,
+                             const int32_t* slot_token, const int32_t* tiles,
+                             const int32_t* meta, int64_t max_tiles, int64_t T, int64_t H,
+                             int64_t I, int64_t E, int64_t k, qmoe_bf16* act,
+                             qmoe_bf16* y_slot, qmoe_stream_t stream);
+
+/* Weighted unpermute-combine, deterministic (fixed order j = 0..k-1, fp32):
+ *   out[t] = residual[t] + sum_j topk_w[t,j] * y_slot[token_slot[t*k+j]]
+ *   y_slot: f32 or bf16 (y_is_bf16) [T*k, H]; residual: f32 [T, H] or NULL
+ *   (may alias out); out: f32 [T, H].
+ * Replaces: the affinity multiply + scatter-add of the right kernel
+ *   (_allblk_fused_down_aff_scatter qwen_with_nki.py:4583-4710; fp32
+ *   accumulator variant 5043-5121) and the decode sum(out * aff) 3467-3478,
+ *   plus the residual add at 10207. */
+int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slot,
+                     const float* topk_w, const float* residual, int64_t T, int64_t k,
+                     int64_t H, float* out, qmoe_stream_t stream);
+
+/* Dense GEMM C = A . B^T with an epilogue mode (QMOE_GEMM_*); bf16 inputs,
+ * fp32 accumulation.  A: bf16 [M, K] (row stride lda); B: bf16 [N, K];
+ * C: [M, N] with row stride ldc.  Limits: K % 64 == 0, N % 128 == 0 when
+ * M > 16; K % 512 == 0 when M <= 16 (GEMV path).
+ * Replaces: the o_proj / lm_head ColumnParallelLinear projections of the
+ *   NxDI attention base and model (qwen_with_nki.py:10277-10282);
+ *   _nki_lm_head_kernel 1766-1805. */
+int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+              int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream);
+
+/* QKV projection with per-head RMSNorm over head_dim and RoPE fused into the
+ * epilogue; K/V written straight into the contiguous cache.
+ *   x: bf16 [B*S, H]; wqkv: bf16 [(Hq+2*Hkv)*D, H] (q rows, then k, then v);
+ *   q_norm_w, k_norm_w: bf16 [D]; rope_cos, rope_sin: f32 [max_pos, D/2];
+ *   positions: i32 [B*S] (RoPE position == cache index of the token);
+ *   q_out: bf16 [B*S, Hq, D]; k_cache, v_cache: bf16 [B, Hkv, S_max, D].
+ *   Limits: D == 128, H % 64 == 0, positions < S_max and < max_pos.
+ * Replaces: NeuronQwen3MoEAttention (qwen_with_nki.py:10081-10109): QKV
+ *   projection, q_layernorm/k_layernorm (10102-10103) before RoPE
+ *   (RotaryEmbedding base=rope_theta 10083-10087), KV-cache update. */
+int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv, const qmoe_bf16* q_norm_w,
+                       const qmoe_bf16* k_norm_w, const float* rope_cos, const float* rope_sin,
+                       int64_t max_pos, const int32_t* positions, int64_t B, int64_t S,
+                       int64_t H, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
+                       qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache,
+                       qmoe_stream_t stream);
+
+/* Causal GQA flash attention for a prefill chunk.  Query s of batch b sits at
+ * cache index start + s and sees cache entries [0, start + s].
+ *   q: bf16 [B*S, Hq, D]; k_cache, v_cache: bf16 [B, Hkv, S_max, D];
+ *   out: bf16 [B*S, Hq*D].  Limits: D == 128, Hq % Hkv == 0.
+ * Replaces: the NxDI attention base's context-encoding attention
+ *   (flash kernel attention_isa_kernel, qwen_with_nki.py:25-28, 1251). */
+int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                      int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
+                      int64_t start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
+
+/* Decode attention (split-KV flash decoding), one query per batch row that
+ * sees cache entries [0, ctx_len[b]).
+ *   q: bf16 [B, Hq, D]; ctx_len: i32 [B] (1 <= ctx_len <= S_max);
+ *   partial: f32 workspace of qmoe_attn_decode_workspace(B, Hq, D, S_max) floats;
+ *   out: bf16 [B, Hq*D].  Limits: D == 128, Hq / Hkv <= 16.
+ * Replaces: the NxDI attention base's token-generation attention over the KV
+ *   cache [B, Hkv, S, D] (qwen_with_nki.py:9943-9946). */
+int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t S_max);
+int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                     const int32_t* ctx_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                     int64_t S_max, float scale, float* partial, qmoe_bf16* out,
+                     qmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMOE_CAPI_H */

@@ -1,0 +1,92 @@
+// Shared device/host helpers for libqmoe (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "qmoe_capi.h"
+
+namespace qmoe {
+
+// ---------------------------------------------------------------- errors
+// Records a printf-style message in the thread-local last-error buffer and
+// returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+inline int hip_status(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(QMOE_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+  return QMOE_OK;
+}
+
+#define QMOE_REQUIRE(cond, ...)                              \
+  do {                                                       \
+    if (!(cond)) return ::qmoe::fail(QMOE_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+inline hipStream_t as_stream(qmoe_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- types
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+
+// Round-to-nearest-even float -> bf16 bit pattern (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+// dot of 8 bf16 (packed in a u32x4) with 8 floats
+__device__ __forceinline__ float dot8(const u32x4& w, const float* x) {
+  float s = bf16_lo(w.x) * x[0];
+  s = fmaf(bf16_hi(w.x), x[1], s);
+  s = fmaf(bf16_lo(w.y), x[2], s);
+  s = fmaf(bf16_hi(w.y), x[3], s);
+  s = fmaf(bf16_lo(w.z), x[4], s);
+  s = fmaf(bf16_hi(w.z), x[5], s);
+  s = fmaf(bf16_lo(w.w), x[6], s);
+  s = fmaf(bf16_hi(w.w), x[7], s);
+  return s;
+}
+
+// ---------------------------------------------------------------- reductions (wave64)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Non-temporal 16-byte load for weights that are streamed once.
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+}  // namespace qmoe

@@ -1,0 +1,184 @@
+// Dense bf16 GEMM  C = A . B^T  (A [M,K], B [N,K], fp32 accumulate).
+//
+// Two shapes of work:
+//  * M <= 16 ("GEMV", decode): HBM-bound on B.  The M activation rows are
+//    staged once in LDS; each wave streams R rows of B with 16-byte
+//    non-temporal loads (K/512 loads per row per lane, all in flight), and
+//    reduces the per-lane partial dots with cross-lane shuffles.
+//  * M > 16: the 128x128 MFMA tile engine (mfma_tile.hpp).
+#include "gemm.hpp"
+#include "mfma_tile.hpp"
+
+namespace qmoe {
+
+template <int MODE>
+__device__ __forceinline__ void store_out(void* C, int64_t idx, float v) {
+  if constexpr (MODE == QMOE_GEMM_STORE_BF16) {
+    reinterpret_cast<uint16_t*>(C)[idx] = f32_to_bf16(v);
+  } else if constexpr (MODE == QMOE_GEMM_STORE_F32) {
+    reinterpret_cast<float*>(C)[idx] = v;
+  } else {
+    reinterpret_cast<float*>(C)[idx] += v;
+  }
+}
+
+// ------------------------------------------------------------------ GEMV
+template <int MT, int R, int MODE>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                   const uint16_t* __restrict__ B, int M, int N,
+                                                   int K, void* __restrict__ C, int64_t ldc) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // stage the M activation rows (16-byte chunks)
+  const int kchunks = K / 8;
+  for (int c = t; c < M * kchunks; c += 256) {
+    const int m = c / kchunks, kc = c - m * kchunks;
+    *reinterpret_cast<u32x4*>(xs + m * K + kc * 8) = ld16(A + m * lda + kc * 8);
+  }
+  __syncthreads();
+
+  const int n0 = (blockIdx.x * 4 + wave) * R;
+  float acc[MT][R];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+
+  const uint16_t* brow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) brow[r] = B + int64_t(min(n0 + r, N - 1)) * K;
+
+#pragma unroll 4
+  for (int k = lane * 8; k < K; k += 512) {
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = ld_stream(brow[r] + k);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < M) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + m * K + k);
+        float x8[8] = {bf16_lo(xv.x), bf16_hi(xv.x), bf16_lo(xv.y), bf16_hi(xv.y),
+                       bf16_lo(xv.z), bf16_hi(xv.z), bf16_lo(xv.w), bf16_hi(xv.w)};
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] += dot8(w[r], x8);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m < M) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = wave_sum(acc[m][r]);
+        if (lane == 0 && n0 + r < N) store_out<MODE>(C, int64_t(m) * ldc + n0 + r, v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ MFMA tile
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint16_t* __restrict__ A,
+                                                        int64_t lda,
+                                                        const uint16_t* __restrict__ B, int M,
+                                                        int N, int K, void* __restrict__ C,
+                                                        int64_t ldc) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[tile::SMEM_BYTES / 2];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int m0 = blockIdx.y * tile::BM, n0 = blockIdx.x * tile::BN;
+  const int kc = (t & 7) * 8;
+  const uint16_t* ap[4];
+  const uint16_t* bp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = tile::stage_row(t, j);
+    ap[j] = (m0 + r < M) ? A + int64_t(m0 + r) * lda + kc : nullptr;
+    bp[j] = B + int64_t(n0 + r) * K + kc;
+  }
+  tile::Acc acc;
+  tile::mma_128x128(ap, bp, K, smem, acc);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = n0 + tile::acc_col(wave, lane, ni);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = m0 + tile::acc_row(wave, lane, mi, i);
+        if (row < M) store_out<MODE>(C, int64_t(row) * ldc + col, acc.c[mi][ni][i]);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ launcher
+template <int MODE>
+static int launch_gemv(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                       void* C, int64_t ldc, hipStream_t s) {
+  const size_t shm = size_t(M) * K * 2;
+  const bool wide = N >= 4096;
+  const int rows_per_block = wide ? 16 : 4;
+  dim3 grid((N + rows_per_block - 1) / rows_per_block);
+#define QMOE_GEMV(MT)                                                                        \
+  if (M <= MT) {                                                                             \
+    if (wide)                                                                                \
+      hipLaunchKernelGGL((gemv_kernel<MT, 4, MODE>), grid, dim3(256), shm, s, A, lda, B, M, N, \
+                         K, C, ldc);                                                         \
+    else                                                                                     \
+      hipLaunchKernelGGL((gemv_kernel<MT, 1, MODE>), grid, dim3(256), shm, s, A, lda, B, M, N, \
+                         K, C, ldc);                                                         \
+    return hip_status("qmoe_gemm(gemv)");                                                    \
+  }
+  QMOE_GEMV(1)
+  QMOE_GEMV(2)
+  QMOE_GEMV(4)
+  QMOE_GEMV(8)
+  QMOE_GEMV(16)
+#undef QMOE_GEMV
+  return fail(QMOE_ERR_INVALID, "qmoe_gemm: gemv path needs M <= 16");
+}
+
+int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N,
+                int64_t K, int mode, void* C, int64_t ldc, hipStream_t s) {
+  QMOE_REQUIRE(A && B && C, "qmoe_gemm: null pointer");
+  QMOE_REQUIRE(M > 0 && N > 0 && K > 0, "qmoe_gemm: empty shape M=%lld N=%lld K=%lld",
+               (long long)M, (long long)N, (long long)K);
+  QMOE_REQUIRE(mode >= 0 && mode <= 2, "qmoe_gemm: bad mode %d", mode);
+  QMOE_REQUIRE(lda >= K && ldc >= N, "qmoe_gemm: lda/ldc smaller than the row length");
+  QMOE_REQUIRE(lda % 8 == 0, "qmoe_gemm: lda must be a multiple of 8");
+  QMOE_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31), "qmoe_gemm: dims overflow");
+  if (M <= 16 && M * K <= 32768) {
+    QMOE_REQUIRE(K % 512 == 0, "qmoe_gemm: gemv path needs K %% 512 == 0 (K=%lld)", (long long)K);
+    switch (mode) {
+      case QMOE_GEMM_STORE_BF16:
+        return launch_gemv<QMOE_GEMM_STORE_BF16>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
+      case QMOE_GEMM_STORE_F32:
+        return launch_gemv<QMOE_GEMM_STORE_F32>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
+      default:
+        return launch_gemv<QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
+    }
+  }
+  QMOE_REQUIRE(K % tile::BK == 0, "qmoe_gemm: K %% 64 != 0 (K=%lld)", (long long)K);
+  QMOE_REQUIRE(N % tile::BN == 0, "qmoe_gemm: N %% 128 != 0 (N=%lld)", (long long)N);
+  dim3 grid(N / tile::BN, (M + tile::BM - 1) / tile::BM);
+  switch (mode) {
+    case QMOE_GEMM_STORE_BF16:
+      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_STORE_BF16>, grid, dim3(256), 0, s, A, lda, B,
+                         int(M), int(N), int(K), C, ldc);
+      break;
+    case QMOE_GEMM_STORE_F32:
+      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_STORE_F32>, grid, dim3(256), 0, s, A, lda, B,
+                         int(M), int(N), int(K), C, ldc);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_ADD_F32>, grid, dim3(256), 0, s, A, lda, B,
+                         int(M), int(N), int(K), C, ldc);
+  }
+  return hip_status("qmoe_gemm(tile)");
+}
+
+}  // namespace qmoe
+
+extern "C" int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+                         int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream) {
+  return qmoe::gemm_launch(A, lda, B, M, N, K, mode, C, ldc, qmoe::as_stream(stream));
+}

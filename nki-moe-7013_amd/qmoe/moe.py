@@ -1,0 +1,123 @@
+"""The sparse MoE block on libqmoe kernels.
+
+Host-side mirror of the reference's MoE module surface:
+
+* :class:`MoEBlock` -- router + experts + combine, the body of
+  ``self.mlp(hidden_states, padding_mask)[0]`` in
+  ``NeuronQwen3MoeDecoderLayer.forward`` (qwen_with_nki.py:10206), with the
+  residual add of 10207 fused into the combine.
+* :class:`ExpertMLPs` -- the two expert-dispatch seams the reference patches on
+  NxDI's ``ExpertMLPsV2``: ``forward_selective_loading`` (decode,
+  qwen_with_nki.py:2377, 3456-3478) and ``torch_blockwise_matmul_inference``
+  (prefill, 5872-5881), with the same argument meaning.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+
+# Token counts at or below this use the HBM-bound GEMV experts; above it the
+# MFMA grouped GEMM.  (Each touched expert is streamed once either way.)
+GEMV_MAX_TOKENS = 64
+TILE_M = 128
+
+
+class ExpertMLPs:
+    """Routed SwiGLU experts with packed weights ``w13 [E,2I,H]``, ``w2 [E,H,I]``."""
+
+    def __init__(self, w13: torch.Tensor, w2: torch.Tensor, top_k: int,
+                 normalize_top_k_affinities: bool = True):
+        self.w13 = w13
+        self.w2 = w2
+        self.num_experts = w13.shape[0]
+        self.hidden_size = w13.shape[2]
+        self.intermediate_size = w13.shape[1] // 2
+        self.top_k = top_k
+        self.normalize_top_k_affinities = normalize_top_k_affinities
+
+    def run(self, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
+            residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Permute, run the experts, combine: ``residual + sum_j w_j * expert_j(x)`` (f32)."""
+        T = x.shape[0]
+        route = ops.moe_permute(topk_idx, self.num_experts, TILE_M)
+        if T <= GEMV_MAX_TOKENS:
+            y = ops.moe_experts_gemv(x, self.w13, self.w2, route)
+        else:
+            y = ops.moe_experts_grouped(x, self.w13, self.w2, route)
+        return ops.moe_combine(y, route, topk_w, residual, out)
+
+    # -- reference seams -------------------------------------------------------
+    def forward_selective_loading(self, hidden_states: torch.Tensor, expert_affinities: torch.Tensor,
+                                  expert_index: torch.Tensor) -> torch.Tensor:
+        """Decode seam (qwen_with_nki.py:3456-3478): gather the chosen
+        affinities from ``expert_affinities[T,E]``, L1-normalise them when
+        ``normalize_top_k_affinities``, and return ``sum_j aff_j * mlp_j(x)``
+        as ``[T,H]`` in the input dtype."""
+        T = hidden_states.shape[0]
+        idx = expert_index.to(torch.int32).contiguous()
+        chosen = torch.gather(expert_affinities.float(), 1, expert_index.long())
+        if self.normalize_top_k_affinities:
+            chosen = torch.nn.functional.normalize(chosen, p=1.0, dim=1)
+        out = self.run(hidden_states.to(torch.bfloat16).contiguous(), idx, chosen.contiguous())
+        return out.to(hidden_states.dtype).view(T, -1)
+
+    def torch_blockwise_matmul_inference(self, block_size, num_blocks, hidden_states,
+                                         expert_affinities_masked, token_position_to_id,
+                                         block_to_expert, pad_inputs_for_matmul=False) -> torch.Tensor:
+        """Prefill seam (qwen_with_nki.py:5872-5881, semantics 5728-5789).
+
+        The reference's blocks list, per expert, the token rows routed to it
+        (padding rows point at the extra row ``T``); each selected (token,
+        expert) pair contributes ``mlp_e(x_t) * expert_affinities_masked[t, e]``.
+        The same pairs are recovered here as a top-k list and dispatched
+        through the build's own permutation (a token never repeats within
+        one expert, so the reference's duplicate redirection is not needed).
+        """
+        T, H = hidden_states.shape
+        E = self.num_experts
+        tok = token_position_to_id.view(int(num_blocks), int(block_size)).long()
+        exp = block_to_expert.view(int(num_blocks), 1).long().expand_as(tok)
+        valid = tok < T
+        sel = torch.zeros(T + 1, E, dtype=torch.bool, device=hidden_states.device)
+        sel[tok[valid], exp[valid]] = True
+        sel = sel[:T]
+        k = int(sel.sum(dim=1).max().item()) if T > 0 else 0
+        if k == 0:
+            return torch.zeros_like(hidden_states)
+        # order each token's experts by affinity (descending), like top-k
+        aff = torch.where(sel, expert_affinities_masked.float(), torch.full_like(expert_affinities_masked.float(), -1.0))
+        top_w, top_i = torch.topk(aff, k, dim=1)
+        if not bool((top_w >= 0).all()):
+            raise ValueError("every token must be routed to the same number of experts")
+        out = self.run(hidden_states.to(torch.bfloat16).contiguous(), top_i.to(torch.int32).contiguous(),
+                       top_w.contiguous())
+        return out.to(hidden_states.dtype)
+
+
+class MoEBlock:
+    """Router + experts + combine.  ``forward(x_bf16[T,H], residual_f32[T,H])``
+    returns ``residual + MoE(x)`` in fp32."""
+
+    def __init__(self, w_router: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, top_k: int,
+                 router_bias: Optional[torch.Tensor] = None):
+        self.w_router = w_router
+        self.router_bias = router_bias
+        self.experts = ExpertMLPs(w13, w2, top_k)
+        self.top_k = top_k
+        self.last_routing = None
+
+    def route(self, x: torch.Tensor):
+        logits, topk_w, topk_idx = ops.router_topk(x, self.w_router, self.top_k, self.router_bias)
+        self.last_routing = (logits, topk_w, topk_idx)
+        return logits, topk_w, topk_idx
+
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        _, topk_w, topk_idx = self.route(x)
+        return self.experts.run(x, topk_idx, topk_w, residual, out)
+
+    __call__ = forward

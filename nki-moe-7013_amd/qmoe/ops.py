@@ -1,0 +1,369 @@
+"""Validated torch-facing wrappers over the libqmoe C ABI.
+
+Every wrapper checks device, dtype, contiguity and shape on the host and
+raises ``ValueError`` before anything is launched; outputs and workspaces are
+allocated here with torch (the library itself never allocates).  Work is
+enqueued on torch's current HIP stream and never synchronises the host, so
+every call can be captured into a ``torch.cuda.CUDAGraph``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+I32 = torch.int32
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype, shape=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on a GPU (got {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape must be {tuple(shape)} (got {tuple(t.shape)})")
+
+
+def _same_device(*ts) -> None:
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) > 1:
+        raise ValueError(f"tensors are on different devices: {devs}")
+
+
+# ----------------------------------------------------------------- RMSNorm
+def rmsnorm_residual(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    eps: float,
+    delta: Optional[torch.Tensor] = None,
+    h_out: Optional[torch.Tensor] = None,
+    y_out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``h = x (+ delta)`` (into ``h_out`` if given, may be ``x``); returns
+    ``y = bf16(w * h * rsqrt(mean(h^2) + eps))``."""
+    if x.dim() != 2:
+        raise ValueError("x must be [rows, H]")
+    R, H = x.shape
+    _need(x, "x", F32)
+    _need(w, "w", BF16, (H,))
+    if delta is not None:
+        _need(delta, "delta", F32, (R, H))
+    if h_out is not None:
+        _need(h_out, "h_out", F32, (R, H))
+    if y_out is None:
+        y_out = torch.empty(R, H, dtype=BF16, device=x.device)
+    _need(y_out, "y_out", BF16, (R, H))
+    _same_device(x, w, delta, h_out, y_out)
+    check(
+        lib().qmoe_rmsnorm_residual(
+            _ptr(x), _ptr(delta), _ptr(w), R, H, float(eps), _ptr(h_out), _ptr(y_out), _stream()
+        ),
+        "qmoe_rmsnorm_residual",
+    )
+    return y_out
+
+
+# ----------------------------------------------------------------- router
+def router_topk(
+    x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[torch.Tensor] = None,
+    logits: Optional[torch.Tensor] = None, topk_idx: Optional[torch.Tensor] = None,
+    topk_w: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns ``(logits[T,E] f32, topk_w[T,k] f32, topk_idx[T,k] i32)``."""
+    T, H = x.shape
+    E = w_router.shape[0]
+    _need(x, "x", BF16)
+    _need(w_router, "w_router", BF16, (E, H))
+    if bias is not None:
+        _need(bias, "bias", F32, (E,))
+    dev = x.device
+    logits = torch.empty(T, E, dtype=F32, device=dev) if logits is None else logits
+    topk_idx = torch.empty(T, k, dtype=I32, device=dev) if topk_idx is None else topk_idx
+    topk_w = torch.empty(T, k, dtype=F32, device=dev) if topk_w is None else topk_w
+    _need(logits, "logits", F32, (T, E))
+    _need(topk_idx, "topk_idx", I32, (T, k))
+    _need(topk_w, "topk_w", F32, (T, k))
+    _same_device(x, w_router, bias, logits, topk_idx, topk_w)
+    check(
+        lib().qmoe_router_topk(
+            _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, _ptr(topk_idx), _ptr(topk_w),
+            _ptr(logits), _stream(),
+        ),
+        "qmoe_router_topk",
+    )
+    return logits, topk_w, topk_idx
+
+
+# ----------------------------------------------------------------- dispatch
+@dataclass
+class Route:
+    """Device-side dispatch metadata produced by :func:`moe_permute`."""
+
+    T: int
+    k: int
+    E: int
+    tile_m: int
+    max_tiles: int
+    counts: torch.Tensor  # [E]
+    offsets: torch.Tensor  # [E+1]
+    slot_token: torch.Tensor  # [T*k]
+    token_slot: torch.Tensor  # [T*k]
+    active: torch.Tensor  # [E]
+    tiles: torch.Tensor  # [max_tiles, 4]
+    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, 0)
+
+    @staticmethod
+    def alloc(T: int, k: int, E: int, tile_m: int, device) -> "Route":
+        max_tiles = -(-T * k // tile_m) + E
+        z = lambda *s: torch.empty(*s, dtype=I32, device=device)
+        return Route(T, k, E, tile_m, max_tiles, z(E), z(E + 1), z(T * k), z(T * k), z(E),
+                     z(max_tiles, 4), z(4))
+
+
+def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Optional[Route] = None) -> Route:
+    T, k = topk_idx.shape
+    _need(topk_idx, "topk_idx", I32)
+    if route is None:
+        route = Route.alloc(T, k, E, tile_m, topk_idx.device)
+    if (route.T, route.k, route.E, route.tile_m) != (T, k, E, tile_m):
+        raise ValueError("route buffers were allocated for a different shape")
+    check(
+        lib().qmoe_moe_permute(
+            _ptr(topk_idx), T, k, E, tile_m, route.max_tiles, _ptr(route.counts), _ptr(route.offsets),
+            _ptr(route.slot_token), _ptr(route.token_slot), _ptr(route.active), _ptr(route.tiles),
+            _ptr(route.meta), _stream(),
+        ),
+        "qmoe_moe_permute",
+    )
+    return route
+
+
+# ----------------------------------------------------------------- experts
+def _check_experts(x, w13, w2):
+    T, H = x.shape
+    E, I2, H2 = w13.shape
+    _need(x, "x", BF16)
+    _need(w13, "w13", BF16)
+    if H2 != H or I2 % 2:
+        raise ValueError(f"w13 must be [E, 2I, H={H}] (got {tuple(w13.shape)})")
+    I = I2 // 2
+    _need(w2, "w2", BF16, (E, H, I))
+    return T, H, I, E
+
+
+def moe_experts_gemv(
+    x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, route: Route,
+    act: Optional[torch.Tensor] = None, y_slot: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Decode-shape experts; returns unweighted ``y_slot[T*k, H]`` (f32)."""
+    T, H, I, E = _check_experts(x, w13, w2)
+    if (route.T, route.E) != (T, E):
+        raise ValueError("route does not match x / w13")
+    k = route.k
+    dev = x.device
+    act = torch.empty(T * k, I, dtype=F32, device=dev) if act is None else act
+    y_slot = torch.empty(T * k, H, dtype=F32, device=dev) if y_slot is None else y_slot
+    _need(act, "act", F32, (T * k, I))
+    _need(y_slot, "y_slot", F32, (T * k, H))
+    _same_device(x, w13, w2, route.offsets, act, y_slot)
+    check(
+        lib().qmoe_moe_experts_gemv(
+            _ptr(x), _ptr(w13), _ptr(w2), _ptr(route.offsets), _ptr(route.slot_token),
+            _ptr(route.active), _ptr(route.meta), T, H, I, E, k, _ptr(act), _ptr(y_slot), _stream(),
+        ),
+        "qmoe_moe_experts_gemv",
+    )
+    return y_slot
+
+
+def moe_experts_grouped(
+    x: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, route: Route,
+    act: Optional[torch.Tensor] = None, y_slot: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Prefill-shape experts (MFMA); returns unweighted ``y_slot[T*k, H]`` (bf16)."""
+    T, H, I, E = _check_experts(x, w13, w2)
+    if (route.T, route.E) != (T, E) or route.tile_m != 128:
+        raise ValueError("route must match x / w13 and use tile_m=128")
+    k = route.k
+    dev = x.device
+    act = torch.empty(T * k, I, dtype=BF16, device=dev) if act is None else act
+    y_slot = torch.empty(T * k, H, dtype=BF16, device=dev) if y_slot is None else y_slot
+    _need(act, "act", BF16, (T * k, I))
+    _need(y_slot, "y_slot", BF16, (T * k, H))
+    _same_device(x, w13, w2, route.tiles, act, y_slot)
+    check(
+        lib().qmoe_moe_experts_grouped(
+            _ptr(x), _ptr(w13), _ptr(w2), _ptr(route.slot_token), _ptr(route.tiles), _ptr(route.meta),
+            route.max_tiles, T, H, I, E, k, _ptr(act), _ptr(y_slot), _stream(),
+        ),
+        "qmoe_moe_experts_grouped",
+    )
+    return y_slot
+
+
+def moe_combine(
+    y_slot: torch.Tensor, route: Route, topk_w: torch.Tensor,
+    residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """``out[t] = residual[t] + sum_j topk_w[t,j] * y_slot[token_slot[t*k+j]]`` (f32)."""
+    T, k = route.T, route.k
+    if y_slot.dim() != 2 or y_slot.shape[0] != T * k:
+        raise ValueError("y_slot must be [T*k, H]")
+    H = y_slot.shape[1]
+    if y_slot.dtype not in (F32, BF16):
+        raise ValueError("y_slot must be float32 or bfloat16")
+    _need(y_slot, "y_slot", y_slot.dtype)
+    _need(topk_w, "topk_w", F32, (T, k))
+    if residual is not None:
+        _need(residual, "residual", F32, (T, H))
+    out = torch.empty(T, H, dtype=F32, device=y_slot.device) if out is None else out
+    _need(out, "out", F32, (T, H))
+    _same_device(y_slot, topk_w, residual, out, route.token_slot)
+    check(
+        lib().qmoe_moe_combine(
+            _ptr(y_slot), int(y_slot.dtype == BF16), _ptr(route.token_slot), _ptr(topk_w),
+            _ptr(residual), T, k, H, _ptr(out), _stream(),
+        ),
+        "qmoe_moe_combine",
+    )
+    return out
+
+
+# ----------------------------------------------------------------- GEMM
+def gemm(A: torch.Tensor, B: torch.Tensor, mode: int = _lib.GEMM_STORE_BF16,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``A[M,K] . B[N,K]^T`` with epilogue ``mode`` (store bf16 / store f32 / add f32)."""
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
+        raise ValueError("A must be [M,K] and B [N,K]")
+    M, K = A.shape
+    N = B.shape[0]
+    _need(A, "A", BF16)
+    _need(B, "B", BF16)
+    if out is None:
+        if mode == _lib.GEMM_ADD_F32:
+            raise ValueError("mode ADD_F32 needs out")
+        out = torch.empty(M, N, dtype=BF16 if mode == _lib.GEMM_STORE_BF16 else F32, device=A.device)
+    _need(out, "out", BF16 if mode == _lib.GEMM_STORE_BF16 else F32, (M, N))
+    _same_device(A, B, out)
+    check(lib().qmoe_gemm(_ptr(A), K, _ptr(B), M, N, K, int(mode), _ptr(out), N, _stream()), "qmoe_gemm")
+    return out
+
+
+# ----------------------------------------------------------------- attention
+def qkv_norm_rope(
+    x: torch.Tensor, wqkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+    rope_cos: torch.Tensor, rope_sin: torch.Tensor, positions: torch.Tensor,
+    B: int, S: int, Hq: int, Hkv: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+    eps: float, q_out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """QKV projection + per-head RMSNorm + RoPE; K/V written into the cache.
+    Returns ``q[B*S, Hq, D]`` (bf16)."""
+    T, H = x.shape
+    D = q_norm_w.shape[0]
+    if T != B * S:
+        raise ValueError("x must be [B*S, H]")
+    _need(x, "x", BF16)
+    _need(wqkv, "wqkv", BF16, ((Hq + 2 * Hkv) * D, H))
+    _need(q_norm_w, "q_norm_w", BF16, (D,))
+    _need(k_norm_w, "k_norm_w", BF16, (D,))
+    max_pos = rope_cos.shape[0]
+    _need(rope_cos, "rope_cos", F32, (max_pos, D // 2))
+    _need(rope_sin, "rope_sin", F32, (max_pos, D // 2))
+    _need(positions, "positions", I32, (T,))
+    if k_cache.dim() != 4 or k_cache.shape[:2] != (B, Hkv) or k_cache.shape[3] != D:
+        raise ValueError(f"k_cache must be [B={B}, Hkv={Hkv}, S_max, D={D}]")
+    S_max = k_cache.shape[2]
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    q_out = torch.empty(T, Hq, D, dtype=BF16, device=x.device) if q_out is None else q_out
+    _need(q_out, "q_out", BF16, (T, Hq, D))
+    _same_device(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, k_cache, v_cache, q_out)
+    check(
+        lib().qmoe_qkv_norm_rope(
+            _ptr(x), _ptr(wqkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cos), _ptr(rope_sin),
+            max_pos, _ptr(positions), B, S, H, Hq, Hkv, D, S_max, float(eps), _ptr(q_out),
+            _ptr(k_cache), _ptr(v_cache), _stream(),
+        ),
+        "qmoe_qkv_norm_rope",
+    )
+    return q_out
+
+
+def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, B: int, S: int,
+                 start: int = 0, scale: Optional[float] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal GQA attention of ``q[B*S, Hq, D]`` against the cache; returns ``[B*S, Hq*D]``."""
+    T, Hq, D = q.shape
+    if T != B * S:
+        raise ValueError("q must be [B*S, Hq, D]")
+    _need(q, "q", BF16)
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError("k_cache must be [B, Hkv, S_max, D]")
+    Hkv, S_max = k_cache.shape[1], k_cache.shape[2]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    out = torch.empty(T, Hq * D, dtype=BF16, device=q.device) if out is None else out
+    _need(out, "out", BF16, (T, Hq * D))
+    _same_device(q, k_cache, v_cache, out)
+    check(
+        lib().qmoe_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), B, S, Hq, Hkv, D, S_max,
+                                start, float(scale), _ptr(out), _stream()),
+        "qmoe_attn_prefill",
+    )
+    return out
+
+
+def attn_decode_workspace(B: int, Hq: int, D: int, S_max: int, device) -> torch.Tensor:
+    n = int(lib().qmoe_attn_decode_workspace(B, Hq, D, S_max))
+    return torch.empty(n, dtype=F32, device=device)
+
+
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, ctx_len: torch.Tensor,
+                scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One query per batch row (``q[B, Hq, D]``) over cache entries ``[0, ctx_len[b])``;
+    returns ``[B, Hq*D]``."""
+    B, Hq, D = q.shape
+    _need(q, "q", BF16)
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError("k_cache must be [B, Hkv, S_max, D]")
+    Hkv, S_max = k_cache.shape[1], k_cache.shape[2]
+    _need(ctx_len, "ctx_len", I32, (B,))
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    if workspace is None:
+        workspace = attn_decode_workspace(B, Hq, D, S_max, q.device)
+    need = int(lib().qmoe_attn_decode_workspace(B, Hq, D, S_max))
+    if workspace.dtype != F32 or workspace.numel() < need or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous float32 tensor of >= {need} elements")
+    out = torch.empty(B, Hq * D, dtype=BF16, device=q.device) if out is None else out
+    _need(out, "out", BF16, (B, Hq * D))
+    _same_device(q, k_cache, v_cache, ctx_len, workspace, out)
+    check(
+        lib().qmoe_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ctx_len), B, Hq, Hkv, D,
+                               S_max, float(scale), _ptr(workspace), _ptr(out), _stream()),
+        "qmoe_attn_decode",
+    )
+    return out

@@ -194,9 +194,9 @@ def moe_block_prefill(
     E = gate_up.shape[0]
     logits, top_w, top_i = router_topk(x, w_router, k, bias)
     # expert_affinities_masked[T, E]: renormalised weight where selected, else 0
-    aff = torch.zeros(T, E, dtype=torch.float32)
+    aff = torch.zeros(T, E, dtype=torch.float32, device=x.device)
     aff.scatter_(1, top_i, top_w)
-    out = torch.zeros(T, H, dtype=torch.float32)
+    out = torch.zeros(T, H, dtype=torch.float32, device=x.device)
     xf = x.float()
     for e in range(E):
         tok = torch.nonzero((top_i == e).any(dim=1), as_tuple=False).flatten()
@@ -250,7 +250,9 @@ def rope_tables(head_dim: int, positions: torch.Tensor, theta: float) -> Tuple[t
     inverse frequencies ``theta^(-2i/D)`` and the duplicated-half layout as in
     transformers ``Qwen3MoeRotaryEmbedding`` (default rope parameters).
     """
-    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    inv_freq = 1.0 / (
+        theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=positions.device).float() / head_dim)
+    )
     freqs = positions.float().unsqueeze(-1) * inv_freq
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos(), emb.sin()
@@ -304,10 +306,10 @@ def gqa_attention(q, k, v, q_idx, k_len=None):
     kf = k.float().repeat_interleave(rep, dim=1)
     vf = v.float().repeat_interleave(rep, dim=1)
     scores = (q.float() @ kf.transpose(2, 3)) * (1.0 / math.sqrt(D))
-    kpos = torch.arange(L).view(1, 1, 1, L)
-    mask = kpos > torch.as_tensor(q_idx).view(B, 1, S, 1)
+    kpos = torch.arange(L, device=q.device).view(1, 1, 1, L)
+    mask = kpos > torch.as_tensor(q_idx, device=q.device).view(B, 1, S, 1)
     if k_len is not None:
-        mask = mask | (kpos >= torch.as_tensor(k_len).view(B, 1, 1, 1))
+        mask = mask | (kpos >= torch.as_tensor(k_len, device=q.device).view(B, 1, 1, 1))
     scores = scores.masked_fill(mask, float("-inf"))
     p = torch.softmax(scores, dim=-1, dtype=torch.float32)
     return (p @ vf).transpose(1, 2).contiguous()
@@ -331,7 +333,7 @@ def attention_layer(x, w: Dict[str, torch.Tensor], positions, cfg, past_kv=None)
         past = past_kv[0].shape[2]
         k = torch.cat([past_kv[0].float(), k], dim=2)
         v = torch.cat([past_kv[1].float(), v], dim=2)
-    q_idx = (past + torch.arange(S)).view(1, S).expand(B, S)
+    q_idx = (past + torch.arange(S, device=x.device)).view(1, S).expand(B, S)
     o = gqa_attention(q, k, v, q_idx)
     o = o.reshape(B, S, -1) @ w["o_proj"].float().t()
     return o, (k, v)

@@ -1,0 +1,48 @@
+"""Helpers shared by the GPU parity tests (seeded inputs, tolerance metrics)."""
+
+import sys
+
+import torch
+
+# Parity bars (from the hot path's accuracy contract):
+#   layer / block outputs: max-abs <= 2e-2 and mean relative <= 5e-3 vs fp32
+#   expert indices: bit-exact wherever the k-th / (k+1)-th router logit gap > 1e-3
+MAX_ABS = 2e-2
+MEAN_REL = 5e-3
+GAP = 1e-3
+
+
+def announce(msg: str) -> None:
+    """Name the case before each GPU step (flushed, so a hard failure still shows it)."""
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def mean_rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).abs().mean() / b.abs().mean().clamp_min(1e-30))
+
+
+def max_abs(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.double().cpu() - b.double().cpu()).abs().max())
+
+
+def assert_close_layer(out: torch.Tensor, ref: torch.Tensor, what: str,
+                       max_abs_tol: float = MAX_ABS, mean_rel_tol: float = MEAN_REL) -> None:
+    ma, mr = max_abs(out, ref), mean_rel(out, ref)
+    print(f"  {what}: max_abs={ma:.3e} mean_rel={mr:.3e}", flush=True)
+    assert ma <= max_abs_tol, f"{what}: max abs {ma:.3e} > {max_abs_tol}"
+    assert mr <= mean_rel_tol, f"{what}: mean rel {mr:.3e} > {mean_rel_tol}"
+
+
+def bf16_randn(shape, gen, device, std=1.0):
+    t = torch.empty(shape, dtype=torch.float32, device=device)
+    t.normal_(0.0, std, generator=gen)
+    return t.to(torch.bfloat16)
+
+
+def gap_mask(logits: torch.Tensor, k: int) -> torch.Tensor:
+    """Rows whose k-th and (k+1)-th largest logits differ by more than GAP."""
+    top = torch.topk(logits.float(), k + 1, dim=-1).values
+    return (top[:, k - 1] - top[:, k]) > GAP

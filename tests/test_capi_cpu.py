@@ -1,0 +1,110 @@
+"""CPU-side checks of the C ABI: the library loads, exports every declared
+entry point, and rejects bad arguments before launching anything.
+
+No call here reaches a kernel launch: every call either fails host-side
+validation inside the library (status QMOE_ERR_INVALID) or is rejected by the
+Python wrapper (ValueError) before the library is called.
+"""
+
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+from qmoe import _lib, ops, weights
+
+HEADER = os.path.join(ROOT, "include", "qmoe_capi.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    decl = r"^(?:int|int64_t|const char\*)\s+(qmoe_[a-z0-9_]+)\("
+    return sorted(set(re.findall(decl, text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _declared_symbols()
+    assert len(declared) >= 13
+    for name in declared:
+        assert hasattr(lib, name), f"libqmoe.so does not export {name}"
+    assert set(declared) == set(_lib.PROTOTYPES), "ctypes prototypes out of sync with the header"
+
+
+def test_version():
+    assert _lib.lib().qmoe_version() == 1
+
+
+@pytest.mark.parametrize(
+    "call, msg",
+    [
+        (lambda l: l.qmoe_gemm(None, 64, None, 1, 128, 64, 0, None, 128, None), "null pointer"),
+        (lambda l: l.qmoe_gemm(1, 64, 1, 1, 128, 64, 7, 1, 128, None), "bad mode"),
+        (lambda l: l.qmoe_gemm(1, 104, 1, 40, 128, 100, 0, 1, 128, None), "K % 64"),
+        (lambda l: l.qmoe_rmsnorm_residual(1, None, 1, 4, 6, 1e-6, None, 1, None), "multiple of 4"),
+        (lambda l: l.qmoe_router_topk(1, 1, None, 1, 2048, 300, 8, 1, 1, 1, None), "E must be"),
+        (lambda l: l.qmoe_router_topk(1, 1, None, 1, 2048, 128, 8, 1, 1, None, None), "null pointer"),
+        (lambda l: l.qmoe_moe_permute(1, 4, 8, 128, 128, 10, 1, 1, 1, 1, 1, 1, 1, None), "max_tiles"),
+        (lambda l: l.qmoe_moe_experts_gemv(1, 1, 1, 1, 1, 1, 1, 65, 2048, 768, 128, 8, 1, 1, None), "T must be"),
+        (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2048, 100, 128, 8, 1, 1, None), "I % 64"),
+        (lambda l: l.qmoe_moe_combine(1, 0, 1, 1, None, 4, 8, 6, 1, None), "H % 4"),
+        (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 1, 1, 2048, 32, 4, 64, 10, 1e-6, 1, 1, 1, None), "head_dim"),
+        (lambda l: l.qmoe_attn_prefill(1, 1, 1, 1, 10, 32, 4, 128, 8, 0, 0.1, 1, None), "S_max"),
+        (lambda l: l.qmoe_attn_decode(1, 1, 1, 1, 1, 64, 2, 128, 16, 0.1, 1, 1, None), "Hq / Hkv <= 16"),
+    ],
+)
+def test_invalid_arguments_rejected_before_launch(call, msg):
+    # The pointers here are dummies: never let a case reach a real device.
+    if torch.cuda.is_available():
+        pytest.skip("host-side validation test; runs only where no GPU is visible")
+    rc = call(_lib.lib())
+    assert rc == _lib.QMOE_ERR_INVALID
+    assert msg in _lib.last_error()
+
+
+def test_python_wrappers_reject_host_tensors():
+    a = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.gemm(a, a)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.rmsnorm_residual(torch.zeros(2, 8), torch.zeros(8, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="GPU|dtype"):
+        ops.router_topk(torch.zeros(2, 8), torch.zeros(4, 8, dtype=torch.bfloat16), 2)
+
+
+def test_check_maps_status_to_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.QMOE_ERR_INVALID, "x")
+    with pytest.raises(_lib.QmoeError):
+        _lib.check(_lib.QMOE_ERR_HIP, "x")
+    _lib.check(_lib.QMOE_OK, "x")
+
+
+def test_pack_gate_up_roundtrip_and_layout():
+    import oracle
+
+    g = torch.Generator().manual_seed(0)
+    gu = torch.randn(3, 64, 2 * 96, generator=g)
+    p = weights.pack_gate_up(gu)
+    assert torch.equal(p, oracle.pack_w13(gu, 32))
+    assert torch.equal(weights.unpack_gate_up(p), gu)
+    # packed row 64j + 32 + r is the up row of unit 32j + r
+    assert torch.equal(p[:, 64 + 32 + 5], gu.transpose(1, 2)[:, 96 + 32 + 5])
+
+
+def test_from_hf_experts_matches_reference_conversion():
+    # convert_qwen3_moe_hf_to_neuron_state_dict (qwen_with_nki.py:8928-8990):
+    # gate_up[e] = cat(gate_proj.T, up_proj.T, dim=1); down[e] = down_proj.T
+    g = torch.Generator().manual_seed(1)
+    E, H, I = 2, 16, 64
+    gp = [torch.randn(I, H, generator=g) for _ in range(E)]
+    up = [torch.randn(I, H, generator=g) for _ in range(E)]
+    dp = [torch.randn(H, I, generator=g) for _ in range(E)]
+    w13, w2 = weights.from_hf_experts(gp, up, dp)
+    nxdi_gu = torch.stack([torch.cat([gp[e].t(), up[e].t()], dim=1) for e in range(E)])
+    nxdi_dn = torch.stack([dp[e].t() for e in range(E)])
+    assert torch.equal(weights.unpack_gate_up(w13), nxdi_gu)
+    assert torch.equal(w2, weights.pack_down(nxdi_dn))

@@ -1,0 +1,374 @@
+"""GPU parity tests: every libqmoe kernel against the oracle on the same
+seeded inputs (bf16 inputs are handed to the oracle exactly, upcast to fp32).
+
+Bars: bit-exact for integer / index work; expert indices exact where the
+router-logit gap exceeds 1e-3; floating-point outputs within max-abs 2e-2 and
+mean relative 5e-3 of the fp32 oracle (tighter where noted).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import (GAP, announce, assert_close_layer, bf16_randn, gap_mask, max_abs, mean_rel)
+
+from qmoe import _lib, ops, weights
+from qmoe.moe import MoEBlock
+
+pytestmark = pytest.mark.gpu
+
+H, E, K_TOP, I = 2048, 128, 8, 768
+
+
+@pytest.fixture(autouse=True)
+def _fp32_reference_matmuls():
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+
+
+# --------------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (5, 4096, 2048), (16, 128, 2048), (8, 2048, 4096),
+                                   (128, 256, 2048), (300, 384, 768), (77, 2048, 4096)])
+def test_gemm_vs_fp32(dev, M, N, K):
+    announce(f"gemm M={M} N={N} K={K}")
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N)
+    A = bf16_randn((M, K), g, dev)
+    B = bf16_randn((N, K), g, dev, std=0.02)
+    ref = A.float().cpu() @ B.float().cpu().t()
+    c32 = ops.gemm(A, B, _lib.GEMM_STORE_F32)
+    cbf = ops.gemm(A, B, _lib.GEMM_STORE_BF16)
+    acc = torch.ones(M, N, device=dev)
+    ops.gemm(A, B, _lib.GEMM_ADD_F32, out=acc)
+    torch.cuda.synchronize()
+    scale = float(ref.abs().max())
+    assert max_abs(c32, ref) <= 1e-4 * scale
+    assert max_abs(acc, ref + 1.0) <= 1e-4 * scale + 1e-6
+    # bf16 output: within one bf16 rounding of the fp32 result
+    assert float(((cbf.float().cpu() - ref).abs() - ref.abs() * 2 ** -8).max()) <= 1e-4 * scale
+
+
+# --------------------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("rows", [1, 37, 640])
+def test_rmsnorm_residual(dev, rows):
+    announce(f"rmsnorm rows={rows}")
+    g = torch.Generator(device=dev).manual_seed(rows)
+    x = torch.randn(rows, H, generator=g, device=dev)
+    d = torch.randn(rows, H, generator=g, device=dev)
+    w = bf16_randn((H,), g, dev)
+    h = torch.empty_like(x)
+    y = ops.rmsnorm_residual(x, w, 1e-6, delta=d, h_out=h)
+    y2 = ops.rmsnorm_residual(x, w, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(h, x + d)  # the residual add is one fp32 add: bit-exact
+    ref = oracle.rmsnorm((x + d).cpu(), w.cpu(), 1e-6)
+    ref2 = oracle.rmsnorm(x.cpu(), w.cpu(), 1e-6)
+    # one bf16 rounding of an fp32 value that may differ by a few ulp
+    for out, r in ((y, ref), (y2, ref2)):
+        err = (out.float().cpu() - r).abs() - r.abs() * 2 ** -8
+        assert float(err.max()) <= 1e-5
+
+
+def test_rmsnorm_reference_recipe_on_gpu(dev):
+    """The reference's known-answer recipe (nki_custom_rmsnorm.py:182-214),
+    at H=512: seed 42, x (256,512), w randn, eps 1e-6, max|diff| < 1e-3."""
+    announce("rmsnorm seed-42 recipe")
+    np.random.seed(42)
+    x = np.random.randn(256, 512).astype(np.float32)
+    w = np.random.randn(512).astype(np.float32)
+    wb = torch.from_numpy(w).to(torch.bfloat16)
+    y = ops.rmsnorm_residual(torch.from_numpy(x).to(dev), wb.to(dev), 1e-6)
+    ref = oracle.rmsnorm(torch.from_numpy(x), wb.float(), 1e-6)
+    torch.cuda.synchronize()
+    assert float((y.float().cpu() - ref).abs().max()) < 3e-2  # bf16 output of |y| up to ~8
+    assert float(((y.float().cpu() - ref).abs() - ref.abs() * 2 ** -8).max()) <= 1e-5
+
+
+# --------------------------------------------------------------------------- router
+@pytest.fixture(scope="module")
+def router_w(dev):
+    g = torch.Generator(device=dev).manual_seed(11)
+    return bf16_randn((E, H), g, dev, std=0.02)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 128, 4096])
+def test_router_topk(dev, router_w, T):
+    announce(f"router T={T}")
+    g = torch.Generator(device=dev).manual_seed(100 + T)
+    x = bf16_randn((T, H), g, dev)
+    logits, tw, ti = ops.router_topk(x, router_w, K_TOP)
+    torch.cuda.synchronize()
+    rl, rw, ri = oracle.router_topk(x.cpu(), router_w.cpu(), K_TOP)
+    assert max_abs(logits, rl) <= 1e-4
+    ok = gap_mask(rl, K_TOP)
+    assert ok.float().mean() > 0.5
+    assert torch.equal(ti.cpu().long()[ok], ri[ok])
+    np.testing.assert_allclose(tw.cpu()[ok].numpy(), rw[ok].numpy(), rtol=2e-5, atol=1e-7)
+    np.testing.assert_allclose(tw.sum(-1).cpu().numpy(), 1.0, rtol=1e-5)
+
+
+def test_router_bias_zipf_selection(dev, router_w):
+    announce("router with per-expert bias")
+    T = 256
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = bf16_randn((T, H), g, dev)
+    bias = torch.linspace(2.0, -2.0, E, device=dev)
+    logits, tw, ti = ops.router_topk(x, router_w, K_TOP, bias)
+    torch.cuda.synchronize()
+    rl, rw, ri = oracle.router_topk(x.cpu(), router_w.cpu(), K_TOP, bias.cpu())
+    assert max_abs(logits, rl) <= 1e-4
+    ok = gap_mask(rl, K_TOP)
+    assert torch.equal(ti.cpu().long()[ok], ri[ok])
+
+
+# --------------------------------------------------------------------------- permute
+def _random_topk(T, k, E, seed, skew=None):
+    rng = np.random.default_rng(seed)
+    p = None
+    if skew is not None:
+        p = np.arange(1, E + 1, dtype=np.float64) ** (-skew)
+        p = p[rng.permutation(E)]
+        p /= p.sum()
+    return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+
+
+@pytest.mark.parametrize("T,skew", [(1, None), (8, None), (64, None), (333, None), (4096, None), (4096, 1.1)])
+def test_permute_bit_exact(dev, T, skew):
+    announce(f"permute T={T} skew={skew}")
+    top = _random_topk(T, K_TOP, E, T, skew)
+    route = ops.moe_permute(torch.from_numpy(top).to(dev), E, 128)
+    torch.cuda.synchronize()
+    ref = oracle.moe_permute(top, E, 128)
+    assert torch.equal(route.counts.cpu(), torch.from_numpy(ref["counts"]))
+    assert torch.equal(route.offsets.cpu(), torch.from_numpy(ref["offsets"]))
+    assert torch.equal(route.slot_token.cpu(), torch.from_numpy(ref["slot_token"]))
+    assert torch.equal(route.token_slot.cpu(), torch.from_numpy(ref["token_slot"]))
+    meta = route.meta.cpu()
+    n_tiles, n_active = int(meta[0]), int(meta[1])
+    assert int(meta[2]) == 0
+    assert n_tiles == len(ref["tiles"]) and n_active == len(ref["active"])
+    assert torch.equal(route.tiles.cpu()[:n_tiles, :3], torch.from_numpy(ref["tiles"]))
+    assert torch.equal(route.active.cpu()[:n_active], torch.from_numpy(ref["active"]))
+
+
+def test_permute_rejects_out_of_range_ids(dev):
+    announce("permute with an out-of-range expert id")
+    top = torch.tensor([[0, 1], [2, 200]], dtype=torch.int32, device=dev)
+    route = ops.moe_permute(top, 8, 128)
+    torch.cuda.synchronize()
+    meta = route.meta.cpu()
+    assert int(meta[2]) == 1 and int(meta[0]) == 0 and int(meta[1]) == 0
+    assert sorted(route.token_slot.cpu().tolist()) == [0, 1, 2, 3]
+
+
+# --------------------------------------------------------------------------- experts
+@pytest.fixture(scope="module")
+def experts(dev):
+    g = torch.Generator(device=dev).manual_seed(2024)
+    w13 = bf16_randn((E, 2 * I, H), g, dev, std=0.02)
+    w2 = bf16_randn((E, H, I), g, dev, std=0.02)
+    return w13, w2
+
+
+class _ExpertCache:
+    """Unpacked (NxDI-layout) fp32 expert weights on the CPU, fetched lazily."""
+
+    def __init__(self, w13, w2):
+        self.w13, self.w2, self.c = w13, w2, {}
+
+    def __getitem__(self, e):
+        if e not in self.c:
+            gu = weights.unpack_gate_up(self.w13[e : e + 1]).float().cpu()[0]  # (H, 2I)
+            dn = self.w2[e].float().cpu().t().contiguous()  # (I, H)
+            self.c[e] = (gu, dn)
+        return self.c[e]
+
+
+def _oracle_rows(x, top_i, top_w, cache, rows):
+    """Oracle MoE output for selected token rows (decode schedule, 3456-3478)."""
+    out = []
+    for t in rows:
+        xs = x[t : t + 1].float()
+        acc = torch.stack([oracle.expert_swiglu(xs, *cache[int(e)])[0] for e in top_i[t]])
+        out.append(torch.sum(acc * top_w[t].float().unsqueeze(1), dim=0))
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 128, 512, 4096])
+def test_experts_and_combine(dev, experts, T):
+    """Permute -> experts (GEMV for T <= 64, MFMA grouped above) -> combine,
+    with routing fixed to the same top-k for both sides."""
+    announce(f"experts+combine T={T}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(7 + T)
+    x = bf16_randn((T, H), g, dev)
+    top = torch.from_numpy(_random_topk(T, K_TOP, E, 99 + T)).to(dev)
+    tw = torch.rand(T, K_TOP, generator=g, device=dev)
+    tw = tw / tw.sum(-1, keepdim=True)
+    residual = torch.randn(T, H, generator=g, device=dev)
+    route = ops.moe_permute(top, E, 128)
+    y = ops.moe_experts_gemv(x, w13, w2, route) if T <= 64 else ops.moe_experts_grouped(x, w13, w2, route)
+    out = ops.moe_combine(y, route, tw, residual=residual)
+    torch.cuda.synchronize()
+    rows = list(range(T)) if T <= 128 else sorted(np.random.default_rng(T).choice(T, 96, replace=False).tolist())
+    cache = _ExpertCache(w13, w2)
+    ref = _oracle_rows(x.cpu(), top.cpu(), tw.cpu(), cache, rows)
+    got = (out.cpu() - residual.cpu())[rows]
+    tight = T <= 64  # fp32 activations on the GEMV path
+    assert_close_layer(got, ref, f"moe T={T}", max_abs_tol=2e-3 if tight else 2e-2,
+                       mean_rel_tol=1e-4 if tight else 5e-3)
+
+
+def test_experts_deterministic(dev, experts):
+    announce("experts repeat-run bitwise equality T=512")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(5)
+    T = 512
+    x = bf16_randn((T, H), g, dev)
+    top = torch.from_numpy(_random_topk(T, K_TOP, E, 5, skew=1.1)).to(dev)
+    tw = torch.full((T, K_TOP), 1.0 / K_TOP, device=dev)
+    outs = []
+    for _ in range(2):
+        route = ops.moe_permute(top, E, 128)
+        y = ops.moe_experts_grouped(x, w13, w2, route)
+        outs.append(ops.moe_combine(y, route, tw))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("T", [1, 128])
+def test_moe_block_vs_oracle(dev, experts, router_w, T):
+    """Full block: router -> permute -> experts -> combine vs oracle.moe_block."""
+    announce(f"moe block T={T}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(1000 + T)
+    x = bf16_randn((T, H), g, dev)
+    blk = MoEBlock(router_w, w13, w2, K_TOP)
+    out = blk(x)
+    torch.cuda.synchronize()
+    rl, rw, ri = oracle.router_topk(x.cpu(), router_w.cpu(), K_TOP)
+    ok = gap_mask(rl, K_TOP)
+    _, _, ti = blk.last_routing
+    assert torch.equal(ti.cpu().long()[ok], ri[ok])
+    rows = [t for t in range(T) if bool(ok[t])]
+    ref = _oracle_rows(x.cpu(), ri, rw, _ExpertCache(w13, w2), rows)
+    assert_close_layer(out.cpu()[rows], ref, f"moe block T={T}")
+
+
+def test_expert_seams_match_block(dev, experts, router_w):
+    """forward_selective_loading / torch_blockwise_matmul_inference seams give
+    the block's result for the same routing."""
+    announce("expert seams")
+    w13, w2 = experts
+    T = 96
+    g = torch.Generator(device=dev).manual_seed(42)
+    x = bf16_randn((T, H), g, dev)
+    blk = MoEBlock(router_w, w13, w2, K_TOP)
+    ref = blk(x)
+    logits, tw, ti = blk.last_routing
+    aff = torch.softmax(logits, dim=-1)
+    sel = blk.experts.forward_selective_loading(x, aff, ti)
+    # reference block format: per-expert blocks of B rows, padding row id T
+    B = 16
+    top = ti.long().cpu()
+    blocks, b2e = [], []
+    for e in range(E):
+        toks = torch.nonzero((top == e).any(dim=1)).flatten().tolist()
+        for s in range(0, len(toks), B):
+            chunk = toks[s : s + B]
+            blocks.append(chunk + [T] * (B - len(chunk)))
+            b2e.append(e)
+    masked = torch.zeros(T, E, device=dev)
+    masked.scatter_(1, ti.long(), tw)
+    tpid = torch.tensor(blocks, dtype=torch.long, device=dev).flatten()
+    bw = blk.experts.torch_blockwise_matmul_inference(
+        B, len(blocks), x, masked, tpid, torch.tensor(b2e, device=dev))
+    torch.cuda.synchronize()
+    assert_close_layer(sel.float().cpu(), ref.cpu(), "selective-loading seam", 2e-2, 1e-2)
+    assert_close_layer(bw.float().cpu(), ref.cpu(), "blockwise seam", 2e-2, 1e-2)
+
+
+# --------------------------------------------------------------------------- attention
+HQ, HKV, D = 32, 4, 128
+
+
+@pytest.fixture(scope="module")
+def attn_w(dev):
+    g = torch.Generator(device=dev).manual_seed(77)
+    wqkv = bf16_randn(((HQ + 2 * HKV) * D, H), g, dev, std=0.02)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    return wqkv, qn, kn
+
+
+def _rope(max_pos, dev):
+    cos, sin = oracle.rope_tables(D, torch.arange(max_pos), 1.0e6)
+    return cos[:, : D // 2].contiguous().to(dev), sin[:, : D // 2].contiguous().to(dev)
+
+
+@pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0)])
+def test_qkv_norm_rope(dev, attn_w, B, S, start):
+    announce(f"qkv_norm_rope B={B} S={S} start={start}")
+    wqkv, qn, kn = attn_w
+    S_max = start + S + 3
+    g = torch.Generator(device=dev).manual_seed(B * 1000 + S)
+    x = bf16_randn((B * S, H), g, dev)
+    pos = (start + torch.arange(S, device=dev)).repeat(B).to(torch.int32)
+    cos, sin = _rope(S_max, dev)
+    kc = torch.zeros(B, HKV, S_max, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = ops.qkv_norm_rope(x, wqkv, qn, kn, cos, sin, pos, B, S, HQ, HKV, kc, vc, 1e-6)
+    torch.cuda.synchronize()
+    wq, wk, wv = wqkv.float().cpu().split([HQ * D, HKV * D, HKV * D])
+    rq, rk, rv = oracle.qkv_norm_rope(x.cpu().view(B, S, H), wq, wk, wv, qn.cpu(), kn.cpu(),
+                                      pos.cpu().view(B, S).long(), HQ, HKV, D, 1e-6, 1.0e6)
+    # bf16 outputs: one rounding of an fp32 value
+    def chk(a, r, what):
+        err = (a.float().cpu() - r).abs() - r.abs() * 2 ** -8
+        assert float(err.max()) <= 2e-4, what
+    chk(q.view(B, S, HQ, D).transpose(1, 2), rq, "q")
+    chk(kc[:, :, start : start + S], rk, "k cache")
+    chk(vc[:, :, start : start + S], rv, "v cache")
+    assert float(kc[:, :, :start].abs().sum()) == 0.0 and float(kc[:, :, start + S :].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("B,S,start", [(2, 200, 0), (1, 1024, 0), (2, 70, 130), (8, 64, 0)])
+def test_attn_prefill(dev, B, S, start):
+    announce(f"attn_prefill B={B} S={S} start={start}")
+    S_max = start + S + 17
+    g = torch.Generator(device=dev).manual_seed(S + start)
+    q = bf16_randn((B * S, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    # poison the cache beyond the visible range: must not leak into outputs
+    kc[:, :, start + S :] = float("nan")
+    vc[:, :, start + S :] = float("nan")
+    out = ops.attn_prefill(q, kc, vc, B, S, start)
+    torch.cuda.synchronize()
+    qi = (start + torch.arange(S)).view(1, S).expand(B, S)
+    ref = oracle.gqa_attention(q.cpu().view(B, S, HQ, D).transpose(1, 2),
+                               kc.cpu()[:, :, : start + S], vc.cpu()[:, :, : start + S], qi)
+    assert_close_layer(out.cpu().view(B, S, HQ, D), ref, f"attn_prefill B={B} S={S}",
+                       max_abs_tol=2e-2, mean_rel_tol=5e-3)
+
+
+@pytest.mark.parametrize("ctx", [[1], [300, 1000, 17], [8192] * 2])
+def test_attn_decode(dev, ctx):
+    announce(f"attn_decode ctx={ctx}")
+    B = len(ctx)
+    S_max = max(max(ctx), 256)
+    g = torch.Generator(device=dev).manual_seed(sum(ctx))
+    q = bf16_randn((B, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    cl = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    out = ops.attn_decode(q, kc, vc, cl)
+    torch.cuda.synchronize()
+    for b in range(B):
+        L = ctx[b]
+        ref = oracle.gqa_attention(q.cpu()[b : b + 1].view(1, HQ, 1, D), kc.cpu()[b : b + 1, :, :L],
+                                   vc.cpu()[b : b + 1, :, :L], torch.tensor([[L - 1]]))
+        assert_close_layer(out.cpu()[b].view(HQ, D), ref[0, 0], f"attn_decode ctx={L}",
+                           max_abs_tol=1e-2, mean_rel_tol=5e-3)
