@@ -1,0 +1,337 @@
+"""Benchmark of the Qwen3-30B-A3B MoE block on one MI355X.
+
+Workload (default): the MoE block at decode shape, T=1 token, bf16, all 128
+experts resident, H=2048, I=768, top-8.  48 distinct layers of random-init
+weights (58 GB) are resident and the timed steps rotate through them, so the
+76 MB touched per block call cannot be served from the 256 MB Infinity Cache.
+A step is one MoE block call (router -> dispatch -> experts -> combine with
+the residual add) on the next layer's weights; the 48-call rotation is
+captured once in a HIP graph and replayed.
+
+Prints ONE JSON line.  ``value`` is MoE-block tokens/s (T tokens per step).
+``roofline`` is for the dominant kernel(s): the decode expert GEMV pair
+(gate_up + down, one ``qmoe_moe_experts_gemv`` call), timed with HIP events on
+the stream it runs on, against its algorithmic bytes U * 9,437,184 (U =
+distinct experts touched, measured).  ``cpu_baseline`` is the fp32 CPU oracle
+(the reference's decode schedule) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nki-moe-7013_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "Qwen3-30B-A3B-shape decode tokens/s & MoE-block GB/s (% of HBM peak)"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+H, E, I, K_TOP = 2048, 128, 768, 8
+EXPERT_BYTES = 3 * H * I * 2  # 9,437,184
+ROUTER_BYTES = E * H * 2
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=960)
+    ap.add_argument("--warmup", type=int, default=96)
+    ap.add_argument("--tokens", type=int, default=1, help="T tokens per MoE block call")
+    ap.add_argument("--layers", type=int, default=48, help="distinct weight sets rotated through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--extra", action="store_true", help="also time T=8/64 decode and T=4096 prefill")
+    return ap.parse_args()
+
+
+def git_sha():
+    try:
+        return subprocess.check_output(["git", "rev-parse", "--short", "HEAD"], cwd=ROOT,
+                                       stderr=subprocess.DEVNULL).decode().strip()
+    except Exception:
+        return None
+
+
+def make_layers(n_layers, dev, seed=0):
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        w_router = torch.empty(E, H, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
+        w13 = torch.empty(E, 2 * I, H, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
+        w2 = torch.empty(E, H, I, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
+        layers.append((w_router, w13, w2))
+    return layers
+
+
+def time_graph(fn, steps_per_replay, steps, warmup):
+    """Capture fn() (which performs steps_per_replay steps) in a HIP graph and
+    time ceil(steps / steps_per_replay) replays.  Returns (seconds, steps_done)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # eager warm-up: allocations, lazy init
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    reps_w = max(1, math.ceil(warmup / steps_per_replay))
+    reps = max(1, math.ceil(steps / steps_per_replay))
+    for _ in range(reps_w):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, reps * steps_per_replay, graph
+
+
+def event_time_experts(run_one, n, sleep_cycles=60_000_000):
+    """Average GPU duration of run_one(i) bracketed by HIP events on the
+    current stream.  A spin kernel is queued first so every launch is already
+    enqueued when the GPU reaches it (the events then time GPU work only)."""
+    import torch
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(sleep_cycles)
+    for i in range(n):
+        starts[i].record()
+        run_one(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+    ms.sort()
+    return sum(ms) / len(ms), ms[len(ms) // 2]
+
+
+def bench_decode(layers, T, steps, warmup, dev):
+    import torch
+
+    from qmoe import ops
+    from qmoe.moe import MoEBlock
+
+    L = len(layers)
+    g = torch.Generator(device=dev).manual_seed(1234 + T)
+    xs = [torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+    res = [torch.randn(T, H, generator=g, device=dev) for _ in range(L)]
+    outs = [torch.empty(T, H, device=dev) for _ in range(L)]
+    blocks = [MoEBlock(*w, K_TOP) for w in layers]
+
+    def all_layers():
+        for l in range(L):
+            blocks[l](xs[l], res[l], out=outs[l])
+
+    secs, done, graph = time_graph(all_layers, L, steps, warmup)
+    # routing of each layer (identical every replay): distinct experts touched
+    U = []
+    routes = []
+    for l in range(L):
+        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP)
+        routes.append((ops.moe_permute(ti, E, 128), tw))
+        U.append(int(torch.unique(ti).numel()))
+    # dominant kernels: the expert GEMV pair, timed with HIP events
+    def run_experts(i):
+        l = i % L
+        if T <= 64:
+            ops.moe_experts_gemv(xs[l], layers[l][1], layers[l][2], routes[l][0])
+        else:
+            ops.moe_experts_grouped(xs[l], layers[l][1], layers[l][2], routes[l][0])
+
+    mean_ms, med_ms = event_time_experts(run_experts, 2 * L)
+    u_mean = sum(U) / len(U)
+    expert_bytes = u_mean * EXPERT_BYTES
+    block_bytes = expert_bytes + ROUTER_BYTES + 2 * T * H * 2 + 2 * T * H * 4
+    us_per_step = secs / done * 1e6
+    return {
+        "T": T,
+        "us_per_block": us_per_step,
+        "tokens_per_s": T * done / secs,
+        "U_mean": u_mean,
+        "block_GBps": block_bytes / (us_per_step * 1e-6) / 1e9,
+        "block_frac": block_bytes / (us_per_step * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "experts_us_mean": mean_ms * 1e3,
+        "experts_us_median": med_ms * 1e3,
+        "experts_bytes": expert_bytes,
+        "experts_GBps": expert_bytes / (mean_ms * 1e-3) / 1e9,
+        "secs": secs,
+        "steps": done,
+    }
+
+
+def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
+    """MoE block at prefill shape with Zipf(1.1)-skewed routing (router bias)."""
+    import torch
+
+    from qmoe import ops
+    from qmoe.moe import MoEBlock
+
+    g = torch.Generator(device=dev).manual_seed(77)
+    rank = torch.randperm(E, generator=torch.Generator().manual_seed(5)).float() + 1.0
+    bias = (-zipf_s * torch.log(rank)).to(dev)  # skewed expert popularity (Zipf-like)
+    L = min(4, len(layers))
+    xs = [torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
+    blocks = [MoEBlock(*layers[l], K_TOP, router_bias=bias) for l in range(L)]
+
+    def run():
+        for l in range(L):
+            blocks[l](xs[l])
+
+    secs, done, _ = time_graph(run, L, reps * L, L)
+    counts = []
+    for l in range(L):
+        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
+        counts.append(torch.bincount(ti.long().flatten(), minlength=E))
+    cnt = torch.stack(counts).float().mean(0)
+    routes = []
+    for l in range(L):
+        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
+        routes.append(ops.moe_permute(ti, E, 128))
+
+    def run_experts(i):
+        l = i % L
+        ops.moe_experts_grouped(xs[l], layers[l][1], layers[l][2], routes[l])
+
+    mean_ms, med_ms = event_time_experts(run_experts, 4 * L)
+    flops = T * K_TOP * 2 * 3 * H * I
+    us = secs / done * 1e6
+    return {
+        "T": T,
+        "us_per_block": us,
+        "tokens_per_s": T / (us * 1e-6),
+        "experts_us_mean": mean_ms * 1e3,
+        "experts_TFLOPs": flops / (mean_ms * 1e-3) / 1e12,
+        "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "top_expert_share": float(cnt.max() / cnt.sum()),
+    }
+
+
+def cpu_baseline(layer, seconds, dev):
+    """fp32 CPU oracle (reference decode schedule, qwen_with_nki.py:3456-3478)
+    on one layer's weights: T=1 tokens with fresh random inputs until
+    ``seconds`` of work are done."""
+    import torch
+
+    import oracle
+    from qmoe import weights
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    w_router, w13, w2 = layer
+    router = w_router.float().cpu()
+    gate_up = torch.empty(E, H, 2 * I)
+    for e0 in range(0, E, 16):  # unpack on the GPU in slices, then upcast on the host
+        gate_up[e0 : e0 + 16] = weights.unpack_gate_up(w13[e0 : e0 + 16]).float().cpu()
+    down = w2.transpose(1, 2).float().cpu().contiguous()  # (E, I, H)
+    g = torch.Generator().manual_seed(0)
+    n = 0
+    for _ in range(3):  # warm-up
+        oracle.moe_block_decode(torch.randn(1, H, generator=g), router, gate_up, down, K_TOP)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        x = torch.randn(1, H, generator=g).to(torch.bfloat16)
+        oracle.moe_block_decode(x, router, gate_up, down, K_TOP)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": n / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} single-token MoE blocks (T=1, fp32, one layer's 128 experts), {dt:.1f} s",
+        "cpu": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+              "(multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from qmoe import _lib
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    t_setup = time.perf_counter()
+    layers = make_layers(a.layers, dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] {a.layers} layers of MoE weights resident ({a.layers * E * EXPERT_BYTES / 1e9:.1f} GB), "
+          f"setup {setup_s:.1f}s", file=sys.stderr, flush=True)
+
+    dec = bench_decode(layers, a.tokens, a.steps, a.warmup, dev)
+    print(f"[bench] decode T={a.tokens}: {dec}", file=sys.stderr, flush=True)
+    extra = {}
+    if a.extra:
+        for T in (8, 64):
+            extra[f"decode_T{T}"] = bench_decode(layers, T, 480, 48, dev)
+            print(f"[bench] decode T={T}: {extra[f'decode_T{T}']}", file=sys.stderr, flush=True)
+        extra["prefill_T4096"] = bench_prefill(layers, dev)
+        print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(layers[0], a.cpu_seconds, dev)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    achieved = dec["experts_GBps"]
+    line = {
+        "metric": METRIC,
+        "value": round(dec["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": dec["steps"],
+        "warmup": a.warmup,
+        "ms_per_step": round(dec["us_per_block"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) activations, seeded)",
+        "config": {
+            "workload": f"Qwen3-30B-A3B MoE block, decode T={a.tokens}, H=2048, 128 experts top-8, "
+                        f"I=768, {a.layers} rotating layers resident, HIP-graph replay",
+            "tokens_per_step": a.tokens,
+            "layers_rotated": a.layers,
+            "parallelism": "single GPU",
+        },
+        "moe_block_GBps": round(dec["block_GBps"], 1),
+        "moe_block_hbm_frac": round(dec["block_frac"], 4),
+        "roofline": {
+            "kernel": "moe_gateup_gemv_kernel + moe_down_gemv_kernel (qmoe_moe_experts_gemv)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": dec["experts_bytes"],
+            "launch_us_mean": round(dec["experts_us_mean"], 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra or None,
+        "git": git_sha(),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -63,7 +63,7 @@ int qmoe_rmsnorm_residual(const float* x, const float* delta, const qmoe_bf16* w
  * renormalise the k weights to sum 1.  Ties pick the lower expert index.
  *   x: bf16 [T, H]; w_router: bf16 [E, H]; bias: f32 [E] or NULL
  *   topk_idx: i32 [T, k] (descending weight); topk_w: f32 [T, k];
- *   logits: f32 [T, E] or NULL.   Limits: E <= 256, k <= 16, H % 8 == 0.
+ *   logits: f32 [T, E] (required).  Limits: E <= 256, k <= 16, H % 8 == 0.
  * Replaces: NxDI RouterTopK invoked as mlp.router(normed_hidden)
  *   qwen_with_nki.py:8589-8590 with router dtype fp32 / softmax 9886-9888 and
  *   normalize_top_k_affinities 9894, 2399-2405. */
@@ -77,7 +77,9 @@ int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float*
  *   expert-sorted slot, stable by token); token_slot: i32 [T*k] (slot of pair
  *   t*k+j); active: i32 [E] (experts with rows, ascending);
  *   tiles: i32 [max_tiles, 4] = (expert, slot_begin, slot_end, 0) in chunks of
- *   tile_m rows; meta: i32 [4] = (n_tiles, n_active, 0, 0).
+ *   tile_m rows; meta: i32 [4] = (n_tiles, n_active, error, -): error is 1
+ *   when an id is outside [0, E) (then n_tiles = n_active = 0 and the slot
+ *   maps are the identity); meta[3] is not touched.
  *   max_tiles must be >= ceil(T*k / tile_m) + E.
  * Replaces: the block metadata ExpertMLPsV2 builds for
  *   torch_blockwise_matmul_inference (token_position_to_id / block_to_expert,
@@ -87,12 +89,48 @@ int qmoe_moe_permute(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E,
                      int32_t* slot_token, int32_t* token_slot, int32_t* active,
                      int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
 
-/* Decode expert MLPs (bandwidth-bound GEMV form; each touched expert's weights
- * are streamed once for all tokens routed to it).
+/* Routing in one call: router logits + top-k (as qmoe_router_topk) followed by
+ * the dispatch metadata (as qmoe_moe_permute), same argument meanings.
+ * Replaces: the router + dispatch-metadata step in front of ExpertMLPsV2
+ *   (qwen_with_nki.py:8589-8590, 9886-9894, 5872-5881). */
+int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias, int64_t T,
+                   int64_t H, int64_t E, int64_t k, int64_t tile_m, int64_t max_tiles,
+                   float* logits, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                   int32_t* offsets, int32_t* slot_token, int32_t* token_slot, int32_t* active,
+                   int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
+
+/* The whole MoE block at decode shape (T <= 8) in three launches with no
+ * cross-workgroup synchronisation: router logits (with the post-attention
+ * RMSNorm fused when h is given), gate/up GEMV with the top-k recomputed in
+ * every workgroup (no permutation pass), and the down GEMV with the weighted
+ * combine and residual add:
+ *   xin = x, or bf16(rmsnorm(h) * rms_w) written to x_out
+ *   out[t] = residual[t] + sum_j topk_w[t,j] * expert_{topk_idx[t,j]}(xin[t])
+ *   x: bf16 [T,H] or NULL; h: f32 [T,H] or NULL (exactly one of x, h);
+ *   rms_w: bf16 [H] and x_out: bf16 [T,H] (with h); w_router: bf16 [E,H];
+ *   bias: f32 [E] or NULL; w13: bf16 [E,2I,H] packed; w2: bf16 [E,H,I];
+ *   residual: f32 [T,H] or NULL (may alias out and h); outputs logits f32
+ *   [T,E], topk_idx i32 [T,k], topk_w f32 [T,k]; act: f32 [T*k, I] workspace;
+ *   out: f32 [T,H].  The combine sums j = 0..k-1 in order (deterministic).
+ *   Limits: T <= 8, T*k <= 64, E <= 256, k <= 16, H in {512, 1024, 2048,
+ *   4096}, I % 32 == 0, I <= 1536.
+ * Replaces: the decode MoE path of NeuronQwen3MoeDecoderLayer.forward
+ *   (post_attention_layernorm -> router -> forward_selective_loading ->
+ *   residual add, qwen_with_nki.py:10203-10207, 3456-3478) in the fusion order
+ *   of _nki_fused_moe_block_decoder_forward (8518-8711). */
+int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* rms_w, float eps,
+                          const qmoe_bf16* w_router, const float* bias, const qmoe_bf16* w13,
+                          const qmoe_bf16* w2, const float* residual, int64_t T, int64_t H,
+                          int64_t I, int64_t E, int64_t k, float* logits, int32_t* topk_idx,
+                          float* topk_w, float* act, qmoe_bf16* x_out, float* out,
+                          qmoe_stream_t stream);
+
+/* Decode expert MLPs without the combine (bandwidth-bound GEMV form; each
+ * touched expert's weights are streamed once for all tokens routed to it).
  *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed (QMOE_W13_GROUP);
  *   w2: bf16 [E, H, I]; offsets/slot_token/active/meta from qmoe_moe_permute;
  *   act: f32 [T*k, I] workspace; y_slot: f32 [T*k, H] unweighted expert outputs.
- *   Limits: T*k <= 512 per expert pass, H % 512 == 0, I % 64 == 0.
+ *   Limits: T <= 64, H in {512, 1024, 2048, 4096}, I % 32 == 0, I <= 1536.
  * Replaces: ExpertMLPsV2.forward_selective_loading (decode), restated at
  *   qwen_with_nki.py:3456-3478; _nki_batched_moe_kernel 1847-1982. */
 int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_bf16* w2,

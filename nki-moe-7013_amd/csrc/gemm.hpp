@@ -7,3 +7,15 @@ namespace qmoe {
 int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N,
                 int64_t K, int mode, void* C, int64_t ldc, hipStream_t s);
 }  // namespace qmoe
+
+namespace qmoe {
+// Router logits (GEMM) + per-token top-k (see qmoe_router_topk).
+int router_launch(const uint16_t* x, const uint16_t* w_router, const float* bias, int64_t T,
+                  int64_t H, int64_t E, int64_t k, int32_t* topk_idx, float* topk_w, float* logits,
+                  hipStream_t s);
+// Dispatch metadata (see qmoe_moe_permute).
+int permute_launch(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E, int64_t tile_m,
+                   int64_t max_tiles, int32_t* counts, int32_t* offsets, int32_t* slot_token,
+                   int32_t* token_slot, int32_t* active, int32_t* tiles, int32_t* meta,
+                   hipStream_t s);
+}  // namespace qmoe

@@ -6,11 +6,9 @@
 // followed by the L1 renormalisation of the chosen k.
 #include "common.hpp"
 #include "gemm.hpp"
+#include "topk_impl.hpp"
 
 namespace qmoe {
-
-constexpr int ROUTER_MAX_E = 256;
-constexpr int ROUTER_MAX_K = 16;
 
 __global__ __launch_bounds__(256) void topk_softmax_kernel(float* __restrict__ logits,
                                                            const float* __restrict__ bias, int T,
@@ -21,80 +19,15 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(float* __restrict__ l
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= T) return;
   float* lr = logits + int64_t(tok) * E;
-  float v[ROUTER_MAX_E / 64];
-#pragma unroll
-  for (int j = 0; j < ROUTER_MAX_E / 64; ++j) {
-    const int e = lane + 64 * j;
-    if (e < E) {
-      float l = lr[e];
-      if (bias) {
-        l += bias[e];
-        lr[e] = l;
-      }
-      v[j] = l;
-    } else {
-      v[j] = -INFINITY;
-    }
+  if (bias) {
+    for (int e = lane; e < E; e += 64) lr[e] += bias[e];
   }
-  float top_v[ROUTER_MAX_K];
-  int top_i[ROUTER_MAX_K];
-#pragma unroll
-  for (int r = 0; r < ROUTER_MAX_K; ++r) {
-    if (r >= k) continue;
-    // lane-local best (lowest index on ties: j ascending == e ascending)
-    float bv = v[0];
-    int bi = lane;
-#pragma unroll
-    for (int j = 1; j < ROUTER_MAX_E / 64; ++j) {
-      if (v[j] > bv) {
-        bv = v[j];
-        bi = lane + 64 * j;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    top_v[r] = bv;
-    top_i[r] = bi;
-    if ((bi & 63) == lane) {
-#pragma unroll
-      for (int j = 0; j < ROUTER_MAX_E / 64; ++j)
-        if (bi == lane + 64 * j) v[j] = -INFINITY;
-    }
-  }
-  if (lane == 0) {
-    const float m = top_v[0];
-    float p[ROUTER_MAX_K];
-    float s = 0.0f;
-#pragma unroll
-    for (int r = 0; r < ROUTER_MAX_K; ++r) {
-      if (r < k) {
-        p[r] = expf(top_v[r] - m);
-        s += p[r];
-      }
-    }
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int r = 0; r < ROUTER_MAX_K; ++r) {
-      if (r >= k) continue;
-      topk_idx[int64_t(tok) * k + r] = top_i[r];
-      topk_w[int64_t(tok) * k + r] = p[r] * inv;
-    }
-  }
+  topk_softmax_wave(lr, E, k, topk_idx + int64_t(tok) * k, topk_w + int64_t(tok) * k);
 }
 
-}  // namespace qmoe
-
-extern "C" int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias,
-                                int64_t T, int64_t H, int64_t E, int64_t k, int32_t* topk_idx,
-                                float* topk_w, float* logits, qmoe_stream_t stream) {
-  using namespace qmoe;
+int router_launch(const uint16_t* x, const uint16_t* w_router, const float* bias, int64_t T,
+                  int64_t H, int64_t E, int64_t k, int32_t* topk_idx, float* topk_w, float* logits,
+                  hipStream_t s) {
   QMOE_REQUIRE(x && w_router && topk_idx && topk_w && logits,
                "qmoe_router_topk: null pointer (logits is required)");
   QMOE_REQUIRE(T >= 0 && T < (1ll << 31), "qmoe_router_topk: bad T");
@@ -102,7 +35,6 @@ extern "C" int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, c
   QMOE_REQUIRE(k > 0 && k <= ROUTER_MAX_K && k <= E, "qmoe_router_topk: k must be in [1, min(16, E)]");
   QMOE_REQUIRE(H > 0 && H % 8 == 0, "qmoe_router_topk: H %% 8 != 0");
   if (T == 0) return QMOE_OK;
-  hipStream_t s = as_stream(stream);
   if (T <= 16) {
     QMOE_REQUIRE(H % 512 == 0, "qmoe_router_topk: decode path needs H %% 512 == 0");
   } else {
@@ -113,4 +45,26 @@ extern "C" int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, c
   hipLaunchKernelGGL(topk_softmax_kernel, dim3(unsigned((T + 3) / 4)), dim3(256), 0, s, logits,
                      bias, int(T), int(E), int(k), topk_idx, topk_w);
   return hip_status("qmoe_router_topk");
+}
+
+}  // namespace qmoe
+
+extern "C" int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias,
+                                int64_t T, int64_t H, int64_t E, int64_t k, int32_t* topk_idx,
+                                float* topk_w, float* logits, qmoe_stream_t stream) {
+  return qmoe::router_launch(x, w_router, bias, T, H, E, k, topk_idx, topk_w, logits,
+                             qmoe::as_stream(stream));
+}
+
+extern "C" int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias,
+                              int64_t T, int64_t H, int64_t E, int64_t k, int64_t tile_m,
+                              int64_t max_tiles, float* logits, int32_t* topk_idx, float* topk_w,
+                              int32_t* counts, int32_t* offsets, int32_t* slot_token,
+                              int32_t* token_slot, int32_t* active, int32_t* tiles, int32_t* meta,
+                              qmoe_stream_t stream) {
+  hipStream_t s = qmoe::as_stream(stream);
+  int rc = qmoe::router_launch(x, w_router, bias, T, H, E, k, topk_idx, topk_w, logits, s);
+  if (rc) return rc;
+  return qmoe::permute_launch(topk_idx, T, k, E, tile_m, max_tiles, counts, offsets, slot_token,
+                              token_slot, active, tiles, meta, s);
 }

@@ -109,15 +109,50 @@ class MoEBlock:
         self.experts = ExpertMLPs(w13, w2, top_k)
         self.top_k = top_k
         self.last_routing = None
-
-    def route(self, x: torch.Tensor):
-        logits, topk_w, topk_idx = ops.router_topk(x, self.w_router, self.top_k, self.router_bias)
-        self.last_routing = (logits, topk_w, topk_idx)
-        return logits, topk_w, topk_idx
+        self._bufs = {}
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        _, topk_w, topk_idx = self.route(x)
-        return self.experts.run(x, topk_idx, topk_w, residual, out)
+        """``residual + MoE(x)`` (fp32) for bf16 ``x[T,H]``."""
+        T = x.shape[0]
+        ex = self.experts
+        if T <= ops.DECODE_BLOCK_MAX_T:
+            bufs = self._decode_bufs(T, x.device)
+            out = ops.moe_decode_block(self.w_router, ex.w13, ex.w2, self.top_k, x=x, bias=self.router_bias,
+                                       residual=residual, out=out, bufs=bufs)
+            self.last_routing = (bufs.logits, bufs.topk_w, bufs.topk_idx)
+            return out
+        route = ops.moe_route(x, self.w_router, self.top_k, self.router_bias, TILE_M)
+        self.last_routing = (route.logits, route.topk_w, route.topk_idx)
+        if T <= GEMV_MAX_TOKENS:
+            y = ops.moe_experts_gemv(x, ex.w13, ex.w2, route)
+        else:
+            y = ops.moe_experts_grouped(x, ex.w13, ex.w2, route)
+        return ops.moe_combine(y, route, route.topk_w, residual, out)
+
+    def forward_normed(self, h: torch.Tensor, rms_w: torch.Tensor, eps: float,
+                       residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+        """``residual + MoE(rmsnorm(h) * rms_w)``: the post-attention RMSNorm
+        fused into the router launch when ``T <= 8``."""
+        T = h.shape[0]
+        if T <= ops.DECODE_BLOCK_MAX_T:
+            ex = self.experts
+            bufs = self._decode_bufs(T, h.device)
+            out = ops.moe_decode_block(self.w_router, ex.w13, ex.w2, self.top_k, h=h, rms_w=rms_w, eps=eps,
+                                       bias=self.router_bias, residual=residual, out=out, bufs=bufs)
+            self.last_routing = (bufs.logits, bufs.topk_w, bufs.topk_idx)
+            return out
+        x = ops.rmsnorm_residual(h, rms_w, eps)
+        return self.forward(x, residual, out)
+
+    def _decode_bufs(self, T: int, device) -> "ops.DecodeBlockBuffers":
+        key = (T, str(device))
+        b = self._bufs.get(key)
+        if b is None:
+            ex = self.experts
+            b = ops.DecodeBlockBuffers.alloc(T, ex.hidden_size, ex.intermediate_size, ex.num_experts,
+                                             self.top_k, device)
+            self._bufs[key] = b
+        return b
 
     __call__ = forward

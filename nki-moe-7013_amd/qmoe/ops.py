@@ -130,14 +130,22 @@ class Route:
     token_slot: torch.Tensor  # [T*k]
     active: torch.Tensor  # [E]
     tiles: torch.Tensor  # [max_tiles, 4]
-    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, 0)
+    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, arrival counter)
+    logits: Optional[torch.Tensor] = None  # [T, E] f32 (filled by moe_route)
+    topk_idx: Optional[torch.Tensor] = None  # [T, k] i32
+    topk_w: Optional[torch.Tensor] = None  # [T, k] f32
 
     @staticmethod
-    def alloc(T: int, k: int, E: int, tile_m: int, device) -> "Route":
+    def alloc(T: int, k: int, E: int, tile_m: int, device, with_topk: bool = False) -> "Route":
         max_tiles = -(-T * k // tile_m) + E
         z = lambda *s: torch.empty(*s, dtype=I32, device=device)
-        return Route(T, k, E, tile_m, max_tiles, z(E), z(E + 1), z(T * k), z(T * k), z(E),
-                     z(max_tiles, 4), z(4))
+        r = Route(T, k, E, tile_m, max_tiles, z(E), z(E + 1), z(T * k), z(T * k), z(E),
+                  z(max_tiles, 4), torch.zeros(4, dtype=I32, device=device))
+        if with_topk:
+            r.logits = torch.empty(T, E, dtype=F32, device=device)
+            r.topk_idx = z(T, k)
+            r.topk_w = torch.empty(T, k, dtype=F32, device=device)
+        return r
 
 
 def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Optional[Route] = None) -> Route:
@@ -154,6 +162,32 @@ def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Option
             _ptr(route.meta), _stream(),
         ),
         "qmoe_moe_permute",
+    )
+    return route
+
+
+def moe_route(x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[torch.Tensor] = None,
+              tile_m: int = 128, route: Optional[Route] = None) -> Route:
+    """Router + top-k + dispatch metadata (one launch for T <= 64)."""
+    T, H = x.shape
+    E = w_router.shape[0]
+    _need(x, "x", BF16)
+    _need(w_router, "w_router", BF16, (E, H))
+    if bias is not None:
+        _need(bias, "bias", F32, (E,))
+    if route is None:
+        route = Route.alloc(T, k, E, tile_m, x.device, with_topk=True)
+    if (route.T, route.k, route.E, route.tile_m) != (T, k, E, tile_m) or route.topk_idx is None:
+        raise ValueError("route buffers were allocated for a different shape / without top-k buffers")
+    _same_device(x, w_router, bias, route.meta)
+    check(
+        lib().qmoe_moe_route(
+            _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, tile_m, route.max_tiles, _ptr(route.logits),
+            _ptr(route.topk_idx), _ptr(route.topk_w), _ptr(route.counts), _ptr(route.offsets),
+            _ptr(route.slot_token), _ptr(route.token_slot), _ptr(route.active), _ptr(route.tiles),
+            _ptr(route.meta), _stream(),
+        ),
+        "qmoe_moe_route",
     )
     return route
 
@@ -194,6 +228,79 @@ def moe_experts_gemv(
         "qmoe_moe_experts_gemv",
     )
     return y_slot
+
+
+@dataclass
+class DecodeBlockBuffers:
+    """Outputs / workspace of :func:`moe_decode_block` (allocate once, reuse)."""
+
+    logits: torch.Tensor  # [T, E] f32
+    topk_idx: torch.Tensor  # [T, k] i32
+    topk_w: torch.Tensor  # [T, k] f32
+    act: torch.Tensor  # [T*k, I] f32
+    x_out: torch.Tensor  # [T, H] bf16 (normalised input, when h is given)
+
+    @staticmethod
+    def alloc(T: int, H: int, I: int, E: int, k: int, device) -> "DecodeBlockBuffers":
+        return DecodeBlockBuffers(
+            torch.empty(T, E, dtype=F32, device=device), torch.empty(T, k, dtype=I32, device=device),
+            torch.empty(T, k, dtype=F32, device=device), torch.empty(T * k, I, dtype=F32, device=device),
+            torch.empty(T, H, dtype=BF16, device=device))
+
+
+DECODE_BLOCK_MAX_T = 8
+
+
+def moe_decode_block(
+    w_router: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, k: int, *,
+    x: Optional[torch.Tensor] = None, h: Optional[torch.Tensor] = None,
+    rms_w: Optional[torch.Tensor] = None, eps: float = 1e-6, bias: Optional[torch.Tensor] = None,
+    residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+    bufs: Optional[DecodeBlockBuffers] = None,
+) -> torch.Tensor:
+    """Whole decode MoE block (T <= 8) in three launches:
+    ``out = residual + MoE(x)`` with ``x`` given, or ``x = rmsnorm(h) * rms_w``."""
+    if (x is None) == (h is None):
+        raise ValueError("pass exactly one of x (bf16) and h (f32)")
+    src = x if x is not None else h
+    T, H = src.shape
+    E = w_router.shape[0]
+    if x is not None:
+        _need(x, "x", BF16)
+    else:
+        _need(h, "h", F32)
+        if rms_w is None:
+            raise ValueError("h needs rms_w")
+        _need(rms_w, "rms_w", BF16, (H,))
+    _need(w_router, "w_router", BF16, (E, H))
+    _need(w13, "w13", BF16)
+    if w13.shape[0] != E or w13.shape[2] != H:
+        raise ValueError("w13 must be [E, 2I, H]")
+    I = w13.shape[1] // 2
+    _need(w2, "w2", BF16, (E, H, I))
+    if bias is not None:
+        _need(bias, "bias", F32, (E,))
+    if residual is not None:
+        _need(residual, "residual", F32, (T, H))
+    dev = src.device
+    bufs = DecodeBlockBuffers.alloc(T, H, I, E, k, dev) if bufs is None else bufs
+    _need(bufs.logits, "logits", F32, (T, E))
+    _need(bufs.topk_idx, "topk_idx", I32, (T, k))
+    _need(bufs.topk_w, "topk_w", F32, (T, k))
+    _need(bufs.act, "act", F32, (T * k, I))
+    _need(bufs.x_out, "x_out", BF16, (T, H))
+    out = torch.empty(T, H, dtype=F32, device=dev) if out is None else out
+    _need(out, "out", F32, (T, H))
+    _same_device(src, w_router, w13, w2, bias, residual, out, bufs.act)
+    check(
+        lib().qmoe_moe_decode_block(
+            _ptr(x), _ptr(h), _ptr(rms_w), float(eps), _ptr(w_router), _ptr(bias), _ptr(w13), _ptr(w2),
+            _ptr(residual), T, H, I, E, k, _ptr(bufs.logits), _ptr(bufs.topk_idx), _ptr(bufs.topk_w),
+            _ptr(bufs.act), _ptr(bufs.x_out), _ptr(out), _stream(),
+        ),
+        "qmoe_moe_decode_block",
+    )
+    return out
 
 
 def moe_experts_grouped(

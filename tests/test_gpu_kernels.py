@@ -372,3 +372,69 @@ def test_attn_decode(dev, ctx):
                                    vc.cpu()[b : b + 1, :, :L], torch.tensor([[L - 1]]))
         assert_close_layer(out.cpu()[b].view(HQ, D), ref[0, 0], f"attn_decode ctx={L}",
                            max_abs_tol=1e-2, mean_rel_tol=5e-3)
+
+
+# --------------------------------------------------------------------------- fused decode path
+@pytest.mark.parametrize("T", [1, 3, 8, 17, 64, 65, 300])
+def test_moe_route_fused(dev, router_w, T):
+    """qmoe_moe_route (one launch for T <= 64) == router_topk + permute, and
+    its arrival counter is re-armed (three calls in a row agree)."""
+    announce(f"moe_route T={T}")
+    g = torch.Generator(device=dev).manual_seed(500 + T)
+    x = bf16_randn((T, H), g, dev)
+    route = ops.Route.alloc(T, K_TOP, E, 128, dev, with_topk=True)
+    for rep in range(3):
+        ops.moe_route(x, router_w, K_TOP, None, 128, route=route)
+        torch.cuda.synchronize()
+        assert int(route.meta[3]) == 0, "arrival counter not re-armed"
+        rl, rw, ri = oracle.router_topk(x.cpu(), router_w.cpu(), K_TOP)
+        assert max_abs(route.logits, rl) <= 1e-4
+        ok = gap_mask(rl, K_TOP)
+        assert torch.equal(route.topk_idx.cpu().long()[ok], ri[ok])
+        np.testing.assert_allclose(route.topk_w.cpu()[ok].numpy(), rw[ok].numpy(), rtol=2e-5, atol=1e-7)
+        ref = oracle.moe_permute(route.topk_idx.cpu().numpy(), E, 128)
+        assert torch.equal(route.slot_token.cpu(), torch.from_numpy(ref["slot_token"]))
+        assert torch.equal(route.token_slot.cpu(), torch.from_numpy(ref["token_slot"]))
+        assert torch.equal(route.offsets.cpu(), torch.from_numpy(ref["offsets"]))
+        n_act = int(route.meta[1])
+        assert torch.equal(route.active.cpu()[:n_act], torch.from_numpy(ref["active"]))
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 8])
+@pytest.mark.parametrize("normed", [False, True])
+def test_moe_decode_block(dev, experts, router_w, T, normed):
+    """Three-launch decode block: routing exact where the gap allows, output
+    vs the oracle, repeat calls bitwise equal, in-place residual."""
+    announce(f"moe_decode_block T={T} normed={normed}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(900 + T)
+    h = torch.randn(T, H, generator=g, device=dev)
+    rms_w = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    residual = torch.randn(T, H, generator=g, device=dev)
+    bufs = ops.DecodeBlockBuffers.alloc(T, H, I, E, K_TOP, dev)
+    if normed:
+        x_ref = oracle.rmsnorm(h.cpu(), rms_w.cpu(), 1e-6).to(torch.bfloat16)
+        run = lambda res, out: ops.moe_decode_block(router_w, w13, w2, K_TOP, h=h, rms_w=rms_w, eps=1e-6,
+                                                    residual=res, out=out, bufs=bufs)
+    else:
+        x = h.to(torch.bfloat16)
+        x_ref = x.cpu()
+        run = lambda res, out: ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x, residual=res,
+                                                    out=out, bufs=bufs)
+    outs = [run(residual, None) for _ in range(3)]
+    inplace = residual.clone()
+    run(inplace, inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert torch.equal(outs[0], inplace)
+    if normed:  # the fused RMSNorm output: one bf16 rounding of the fp32 value
+        err = (bufs.x_out.float().cpu() - oracle.rmsnorm(h.cpu(), rms_w.cpu(), 1e-6)).abs()
+        assert float((err - x_ref.float().abs() * 2 ** -8).max()) <= 1e-5
+    xin = bufs.x_out.cpu() if normed else x_ref
+    rl, rw, ri = oracle.router_topk(xin, router_w.cpu(), K_TOP)
+    assert max_abs(bufs.logits, rl) <= 1e-4
+    ok = gap_mask(rl, K_TOP)
+    assert torch.equal(bufs.topk_idx.cpu().long()[ok], ri[ok])
+    rows = [t for t in range(T) if bool(ok[t])]
+    ref = _oracle_rows(xin, ri, rw, _ExpertCache(w13, w2), rows)
+    assert_close_layer(outs[0].cpu()[rows] - residual.cpu()[rows], ref, f"decode block T={T}", 2e-3, 1e-4)
