@@ -99,11 +99,11 @@ int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* b
                    int32_t* offsets, int32_t* slot_token, int32_t* token_slot, int32_t* active,
                    int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
 
-/* The whole MoE block at decode shape (T <= 8) in three launches with no
- * cross-workgroup synchronisation: router logits (with the post-attention
- * RMSNorm fused when h is given), gate/up GEMV with the top-k recomputed in
- * every workgroup (no permutation pass), and the down GEMV with the weighted
- * combine and residual add:
+/* The whole MoE block at decode shape (T <= 8) in three launches: router
+ * logits + top-k (with the post-attention RMSNorm fused when h is given),
+ * gate/up GEMV (each workgroup picks its expert from the chosen set; no
+ * permutation pass), and the down GEMV with the weighted combine and
+ * residual add:
  *   xin = x, or bf16(rmsnorm(h) * rms_w) written to x_out
  *   out[t] = residual[t] + sum_j topk_w[t,j] * expert_{topk_idx[t,j]}(xin[t])
  *   x: bf16 [T,H] or NULL; h: f32 [T,H] or NULL (exactly one of x, h);
@@ -111,7 +111,9 @@ int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* b
  *   bias: f32 [E] or NULL; w13: bf16 [E,2I,H] packed; w2: bf16 [E,H,I];
  *   residual: f32 [T,H] or NULL (may alias out and h); outputs logits f32
  *   [T,E], topk_idx i32 [T,k], topk_w f32 [T,k]; act: f32 [T*k, I] workspace;
- *   out: f32 [T,H].  The combine sums j = 0..k-1 in order (deterministic).
+ *   sync: i32 [1] arrival counter, 0 before the first call and left 0 (calls
+ *   sharing it must not overlap); out: f32 [T,H].  The combine sums
+ *   j = 0..k-1 in order (deterministic).
  *   Limits: T <= 8, T*k <= 64, E <= 256, k <= 16, H in {512, 1024, 2048,
  *   4096}, I % 32 == 0, I <= 1536.
  * Replaces: the decode MoE path of NeuronQwen3MoeDecoderLayer.forward
@@ -122,7 +124,7 @@ int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* r
                           const qmoe_bf16* w_router, const float* bias, const qmoe_bf16* w13,
                           const qmoe_bf16* w2, const float* residual, int64_t T, int64_t H,
                           int64_t I, int64_t E, int64_t k, float* logits, int32_t* topk_idx,
-                          float* topk_w, float* act, qmoe_bf16* x_out, float* out,
+                          float* topk_w, float* act, int32_t* sync, qmoe_bf16* x_out, float* out,
                           qmoe_stream_t stream);
 
 /* Decode expert MLPs without the combine (bandwidth-bound GEMV form; each

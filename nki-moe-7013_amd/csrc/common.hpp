@@ -68,16 +68,38 @@ __device__ __forceinline__ float dot8(const u32x4& w, const float* x) {
 }
 
 // ---------------------------------------------------------------- reductions (wave64)
+// DPP-based: row_shr 1/2/4/8 leave each 16-lane row's total in its lane 15,
+// row_bcast:15 / row_bcast:31 fold the rows so lane 63 holds the wave total,
+// which readlane broadcasts.  Each step is a VALU op with a DPP modifier (a few
+// cycles), unlike __shfl_xor, which goes through ds_bpermute.
+#define QMOE_DPP_ROW_SHR(n) (0x110 + (n))
+#define QMOE_DPP_ROW_BCAST15 0x142
+#define QMOE_DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xf, BOUND_ZERO));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_mov<QMOE_DPP_ROW_SHR(1), 0xf, true>(0.0f, v);
+  v += dpp_mov<QMOE_DPP_ROW_SHR(2), 0xf, true>(0.0f, v);
+  v += dpp_mov<QMOE_DPP_ROW_SHR(4), 0xf, true>(0.0f, v);
+  v += dpp_mov<QMOE_DPP_ROW_SHR(8), 0xf, true>(0.0f, v);
+  v += dpp_mov<QMOE_DPP_ROW_BCAST15, 0xa, false>(0.0f, v);
+  v += dpp_mov<QMOE_DPP_ROW_BCAST31, 0xc, false>(0.0f, v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_SHR(1), 0xf, false>(v, v));
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_SHR(2), 0xf, false>(v, v));
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_SHR(4), 0xf, false>(v, v));
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_SHR(8), 0xf, false>(v, v));
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_BCAST15, 0xa, false>(v, v));
+  v = fmaxf(v, dpp_mov<QMOE_DPP_ROW_BCAST31, 0xc, false>(v, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }

@@ -1,21 +1,21 @@
-// The whole MoE block at decode shape (T <= 8 tokens) in three launches,
-// with no cross-workgroup synchronisation inside any kernel:
+// The whole MoE block at decode shape (T <= 8 tokens) in three launches:
 //
-//   block_router_kernel     [optional post-attention RMSNorm] + router logits.
+//   block_router_kernel     [optional post-attention RMSNorm] + router logits:
 //                           ceil(E/4) workgroups, one wave per router row (kept
 //                           in registers); every workgroup normalises the few
 //                           token rows itself, workgroup 0 also stores them.
-//   block_gateup_kernel     per-token softmax/top-k recomputed redundantly by
-//                           every workgroup from the logits (a few hundred
-//                           bytes), so no permutation kernel is needed: the
-//                           workgroup's active-expert index picks its expert
-//                           from the selected set, and its token rows are the
-//                           (t, j) pairs routed there.  Then the gate/up GEMV
-//                           (weights streamed once into registers) and SwiGLU:
-//                           act[t*k+j, i] (fp32).  Workgroup (0,0) publishes
-//                           top-k for the next kernel and the caller.
-//   block_down_combine_kernel  one workgroup per 8 output columns h, over all
-//                           (t, j) pairs: out[t,h] = residual[t,h] +
+//                           The last workgroup to arrive (device-scope counter,
+//                           re-armed by that workgroup) runs softmax/top-k per
+//                           token.  Only ceil(E/4) = 32 workgroups fence, which
+//                           keeps the serialised fence cost to about 2 us.
+//   block_gateup_kernel     the workgroup's active-expert index selects its
+//                           expert from the set of chosen experts (a bitmask
+//                           built from the few top-k ids) and its token rows are
+//                           the (t, j) pairs routed there, so no permutation
+//                           pass is needed.  Gate/up rows are streamed once into
+//                           registers; SwiGLU in fp32: act[t*k+j, i].
+//   block_down_combine_kernel  one workgroup per 4 output columns h (one per
+//                           wave) over all (t, j) pairs: out[t,h] = residual +
 //                           sum_j w[t,j] * act[t*k+j] . W2[e(t,j), h], summed in
 //                           fixed j order (deterministic; no atomics).
 //
@@ -27,18 +27,21 @@
 namespace qmoe {
 
 constexpr int BLK_MAX_T = 8;
-constexpr int BLK_MAX_PAIRS = 64;  // T * k
-constexpr int BLK_DOWN_ROWS = 8;   // output columns per down workgroup (2 per wave)
-constexpr int BLK_PAIR_GROUP = 8;  // (t, j) pairs whose W2 rows are loaded together
+constexpr int BLK_MAX_PAIRS = 64;         // T * k
+constexpr int BLK_DOWN_ROWS = 4;          // output columns per down workgroup (1 per wave)
+constexpr int BLK_PAIR_GROUP = 8;         // (t, j) pairs whose W2 rows are loaded together
+constexpr int BLK_ACT_LDS_FLOATS = 8192;  // act staged in LDS when T*k*I fits (32 KB)
 
-// ------------------------------------------------------------------ router
+// ------------------------------------------------------------------ router + top-k
 template <int HC>
 __global__ __launch_bounds__(256) void block_router_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ h, const uint16_t* __restrict__ rms_w,
     float eps, const uint16_t* __restrict__ w_router, const float* __restrict__ bias, int T, int H,
-    int E, float* __restrict__ logits, uint16_t* __restrict__ x_out) {
+    int E, int k, float* logits, uint16_t* __restrict__ x_out, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_w, int32_t* sync) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [T][H]
   __shared__ float red[BLK_MAX_T][4];
+  __shared__ int s_last;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int e = blockIdx.x * 4 + wave;
   u32x4 wr[HC];
@@ -48,17 +51,16 @@ __global__ __launch_bounds__(256) void block_router_kernel(
   }
   if (h) {
     // fused RMSNorm: pass 1 sums of squares, pass 2 normalise (rows are L2-hot)
-    float ss[BLK_MAX_T];
 #pragma unroll
     for (int r = 0; r < BLK_MAX_T; ++r) {
-      ss[r] = 0.0f;
       if (r < T) {
+        float ss = 0.0f;
         for (int c = t; c < H / 4; c += 256) {
           const float4 v = reinterpret_cast<const float4*>(h + int64_t(r) * H)[c];
-          ss[r] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+          ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
-        ss[r] = wave_sum(ss[r]);
-        if (lane == 0) red[r][wave] = ss[r];
+        ss = wave_sum(ss);
+        if (lane == 0) red[r][wave] = ss;
       }
     }
     __syncthreads();
@@ -78,47 +80,55 @@ __global__ __launch_bounds__(256) void block_router_kernel(
     stage_rows_bf16(xs, x, nullptr, 0, T, H);
   }
   __syncthreads();
-  if (e >= E) return;
-  const float b = bias ? bias[e] : 0.0f;
-  for (int r = 0; r < T; ++r) {
-    float acc = 0.0f;
+  if (e < E) {
+    const float b = bias ? bias[e] : 0.0f;
+    for (int r = 0; r < T; ++r) {
+      float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < HC; ++c) {
-      opaque(wr[c]);
-      float xf[8];
-      unpack8(*reinterpret_cast<const u32x4*>(xs + r * H + c * 512 + lane * 8), xf);
-      acc += dot8(wr[c], xf);
+      for (int c = 0; c < HC; ++c) {
+        opaque(wr[c]);
+        float xf[8];
+        unpack8(*reinterpret_cast<const u32x4*>(xs + r * H + c * 512 + lane * 8), xf);
+        acc += dot8(wr[c], xf);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) logits[int64_t(r) * E + e] = acc + b;
     }
-    acc = wave_sum(acc);
-    if (lane == 0) logits[int64_t(r) * E + e] = acc + b;
   }
+  // the last workgroup to arrive selects the experts
+  __threadfence();
+  __syncthreads();
+  if (t == 0) s_last = (atomicAdd(sync, 1) == int(gridDim.x) - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  // stage each token's logits in LDS with vector loads, then rank them there
+  float* s_log = reinterpret_cast<float*>(xs);  // T*E floats <= 8 KB, fits in the x staging area
+  for (int q = t; q < T * E; q += 256) s_log[q] = logits[q];
+  __syncthreads();
+  for (int tok = wave; tok < T; tok += 4)
+    topk_softmax_wave(s_log + tok * E, E, k, topk_idx + tok * k, topk_w + tok * k);
+  if (t == 0) *sync = 0;  // every workgroup has arrived: re-arm
 }
 
 // ------------------------------------------------------------------ gate/up
 template <int HC>
 __global__ __launch_bounds__(256) void block_gateup_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ logits, const uint16_t* __restrict__ w13,
-    int T, int H, int I, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
-    float* __restrict__ act) {
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ topk_idx,
+    const uint16_t* __restrict__ w13, int T, int H, int I, int k, float* __restrict__ act) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [min(T*k,16)][H]
   __shared__ int32_t s_idx[BLK_MAX_PAIRS];
-  __shared__ float s_w[BLK_MAX_PAIRS];
   __shared__ uint32_t s_mask[ROUTER_MAX_E / 32];
   __shared__ int32_t s_list[BLK_MAX_PAIRS];
   __shared__ int s_e, s_n;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int npairs = T * k;
   if (t < ROUTER_MAX_E / 32) s_mask[t] = 0u;
-  for (int tok = wave; tok < T; tok += 4)
-    topk_softmax_wave(logits + int64_t(tok) * E, E, k, s_idx + tok * k, s_w + tok * k);
   __syncthreads();
   if (t < npairs) {
-    const int ee = s_idx[t];
+    const int ee = topk_idx[t];
+    s_idx[t] = ee;
     atomicOr(&s_mask[ee >> 5], 1u << (ee & 31));
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-      topk_idx[t] = ee;
-      topk_w[t] = s_w[t];
-    }
   }
   __syncthreads();
   if (t == 0) {
@@ -199,39 +209,46 @@ __global__ __launch_bounds__(256) void block_down_combine_kernel(
     const float* residual, int T, int H, int I, int k, float* out) {
   __shared__ int32_t s_idx[BLK_MAX_PAIRS];
   __shared__ float s_w[BLK_MAX_PAIRS];
-  __shared__ float s_acc[BLK_MAX_T][BLK_DOWN_ROWS];
+  __shared__ __attribute__((aligned(16))) float s_act[BLK_ACT_LDS_FLOATS];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int npairs = T * k;
-  const int h0 = blockIdx.x * BLK_DOWN_ROWS;
+  const int hrow = blockIdx.x * BLK_DOWN_ROWS + wave;
+  const int ichunks = I / 8;
+  // first group's W2 rows go out before anything else (expert ids read directly)
+  u32x4 w[BLK_PAIR_GROUP][IC];
+  auto load_group = [&](int p0) {
+#pragma unroll
+    for (int g = 0; g < BLK_PAIR_GROUP; ++g) {
+      const int p = p0 + g;
+      const int e = p < npairs ? topk_idx[p] : 0;
+      const uint16_t* rowp = w2 + (int64_t(e) * H + hrow) * I;
+#pragma unroll
+      for (int c = 0; c < IC; ++c) {
+        const int ch = lane + 64 * c;
+        w[g][c] = (p < npairs && ch < ichunks) ? ld_stream(rowp + ch * 8) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  load_group(0);
   if (t < npairs) {
     s_idx[t] = topk_idx[t];
     s_w[t] = topk_w[t];
   }
-  if (t < BLK_MAX_T * BLK_DOWN_ROWS) (&s_acc[0][0])[t] = 0.0f;
+  const bool act_lds = npairs * I <= BLK_ACT_LDS_FLOATS;
+  if (act_lds) {
+    for (int q = t; q < npairs * I / 4; q += 256)
+      reinterpret_cast<float4*>(s_act)[q] = reinterpret_cast<const float4*>(act)[q];
+  }
   __syncthreads();
-  const int ichunks = I / 8;
+  float run = 0.0f;  // running weighted sum of the current token (wave-uniform)
   for (int p0 = 0; p0 < npairs; p0 += BLK_PAIR_GROUP) {
-    u32x4 w[BLK_PAIR_GROUP][2][IC];
-#pragma unroll
-    for (int g = 0; g < BLK_PAIR_GROUP; ++g) {
-      const int p = p0 + g;
-      const int e = p < npairs ? s_idx[p] : 0;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const uint16_t* rowp = w2 + (int64_t(e) * H + h0 + 2 * wave + r) * I;
-#pragma unroll
-        for (int c = 0; c < IC; ++c) {
-          const int ch = lane + 64 * c;
-          w[g][r][c] = (p < npairs && ch < ichunks) ? ld_stream(rowp + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
+    if (p0 > 0) load_group(p0);
 #pragma unroll
     for (int g = 0; g < BLK_PAIR_GROUP; ++g) {
       const int p = p0 + g;
       if (p < npairs) {
-        float acc[2] = {0.0f, 0.0f};
-        const float* ap = act + int64_t(p) * I;
+        const float* ap = act_lds ? s_act + p * I : act + int64_t(p) * I;
+        float acc = 0.0f;
 #pragma unroll
         for (int c = 0; c < IC; ++c) {
           const int ch = lane + 64 * c;
@@ -239,25 +256,18 @@ __global__ __launch_bounds__(256) void block_down_combine_kernel(
             const float4 a0 = reinterpret_cast<const float4*>(ap + ch * 8)[0];
             const float4 a1 = reinterpret_cast<const float4*>(ap + ch * 8)[1];
             const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            acc[0] += dot8(w[g][0][c], x8);
-            acc[1] += dot8(w[g][1][c], x8);
+            acc += dot8(w[g][c], x8);
           }
         }
-        acc[0] = wave_sum(acc[0]);
-        acc[1] = wave_sum(acc[1]);
-        if (lane == 0) {
-          const int tok = p / k;
-          s_acc[tok][2 * wave] = fmaf(s_w[p], acc[0], s_acc[tok][2 * wave]);
-          s_acc[tok][2 * wave + 1] = fmaf(s_w[p], acc[1], s_acc[tok][2 * wave + 1]);
+        acc = wave_sum(acc);
+        const int j = p % k;
+        run = (j == 0) ? s_w[p] * acc : fmaf(s_w[p], acc, run);
+        if (j == k - 1 && lane == 0) {
+          const int64_t o = int64_t(p / k) * H + hrow;
+          out[o] = (residual ? residual[o] : 0.0f) + run;
         }
       }
     }
-  }
-  __syncthreads();
-  if (t < T * BLK_DOWN_ROWS) {
-    const int tok = t / BLK_DOWN_ROWS, c = t % BLK_DOWN_ROWS;
-    const int64_t o = int64_t(tok) * H + h0 + c;
-    out[o] = (residual ? residual[o] : 0.0f) + s_acc[tok][c];
   }
 }
 
@@ -270,9 +280,9 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
                                      const qmoe_bf16* w13, const qmoe_bf16* w2,
                                      const float* residual, int64_t T, int64_t H, int64_t I,
                                      int64_t E, int64_t k, float* logits, int32_t* topk_idx,
-                                     float* topk_w, float* act, qmoe_bf16* x_out, float* out,
-                                     qmoe_stream_t stream) {
-  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && act && out,
+                                     float* topk_w, float* act, int32_t* sync, qmoe_bf16* x_out,
+                                     float* out, qmoe_stream_t stream) {
+  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && act && sync && out,
                "qmoe_moe_decode_block: null pointer");
   QMOE_REQUIRE((x != nullptr) != (h != nullptr), "qmoe_moe_decode_block: pass exactly one of x and h");
   QMOE_REQUIRE(!h || (rms_w && x_out), "qmoe_moe_decode_block: h needs rms_w and x_out");
@@ -286,7 +296,7 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
   if (T == 0) return QMOE_OK;
   hipStream_t s = as_stream(stream);
   const uint16_t* xin = h ? x_out : x;
-  const size_t shm0 = size_t(T) * H * 2;
+  const size_t shm0 = std::max<size_t>(size_t(T) * H * 2, size_t(T) * E * 4);
   dim3 g0(unsigned((E + 3) / 4));
   const size_t shm1 = size_t(std::min<int64_t>(T * k, DEC_TOK_CHUNK)) * H * 2;
   dim3 g1(unsigned(std::min<int64_t>(E, T * k)), unsigned(I / 8));
@@ -294,10 +304,11 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
 #define QMOE_BLK(HC)                                                                              \
   case HC:                                                                                        \
     hipLaunchKernelGGL(block_router_kernel<HC>, g0, dim3(256), shm0, s, x, h, rms_w, eps,         \
-                       w_router, bias, int(T), int(H), int(E), logits, x_out);                    \
+                       w_router, bias, int(T), int(H), int(E), int(k), logits, x_out, topk_idx,   \
+                       topk_w, sync);                                                             \
     if (int rc = hip_status("qmoe_moe_decode_block(router)")) return rc;                          \
-    hipLaunchKernelGGL(block_gateup_kernel<HC>, g1, dim3(256), shm1, s, xin, logits, w13, int(T),  \
-                       int(H), int(I), int(E), int(k), topk_idx, topk_w, act);                    \
+    hipLaunchKernelGGL(block_gateup_kernel<HC>, g1, dim3(256), shm1, s, xin, topk_idx, w13,       \
+                       int(T), int(H), int(I), int(k), act);                                      \
     break;
     QMOE_BLK(1)
     QMOE_BLK(2)

@@ -33,7 +33,7 @@ PROTOTYPES = {
     "qmoe_moe_permute": (c_int, [P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
     "qmoe_moe_route": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "qmoe_moe_decode_block": (
-        c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P]),
+        c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
     "qmoe_moe_experts_gemv": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_experts_grouped": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_combine": (c_int, [P, c_int, P, P, P, I64, I64, I64, P, P]),

@@ -239,13 +239,14 @@ class DecodeBlockBuffers:
     topk_w: torch.Tensor  # [T, k] f32
     act: torch.Tensor  # [T*k, I] f32
     x_out: torch.Tensor  # [T, H] bf16 (normalised input, when h is given)
+    sync: torch.Tensor  # [1] i32 arrival counter (zero at rest)
 
     @staticmethod
     def alloc(T: int, H: int, I: int, E: int, k: int, device) -> "DecodeBlockBuffers":
         return DecodeBlockBuffers(
             torch.empty(T, E, dtype=F32, device=device), torch.empty(T, k, dtype=I32, device=device),
             torch.empty(T, k, dtype=F32, device=device), torch.empty(T * k, I, dtype=F32, device=device),
-            torch.empty(T, H, dtype=BF16, device=device))
+            torch.empty(T, H, dtype=BF16, device=device), torch.zeros(1, dtype=I32, device=device))
 
 
 DECODE_BLOCK_MAX_T = 8
@@ -296,7 +297,7 @@ def moe_decode_block(
         lib().qmoe_moe_decode_block(
             _ptr(x), _ptr(h), _ptr(rms_w), float(eps), _ptr(w_router), _ptr(bias), _ptr(w13), _ptr(w2),
             _ptr(residual), T, H, I, E, k, _ptr(bufs.logits), _ptr(bufs.topk_idx), _ptr(bufs.topk_w),
-            _ptr(bufs.act), _ptr(bufs.x_out), _ptr(out), _stream(),
+            _ptr(bufs.act), _ptr(bufs.sync), _ptr(bufs.x_out), _ptr(out), _stream(),
         ),
         "qmoe_moe_decode_block",
     )
