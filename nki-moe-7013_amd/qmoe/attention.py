@@ -1,0 +1,73 @@
+"""GQA attention with qk-RMSNorm + RoPE fused into the QKV epilogue and a
+contiguous per-sequence KV cache, on libqmoe kernels.
+
+Mirrors ``NeuronQwen3MoEAttention`` (qwen_with_nki.py:10081-10109): QKV
+projection -> per-head RMSNorm over head_dim (q_layernorm / k_layernorm,
+10102-10103) -> RoPE with base ``rope_theta`` (10083-10087) -> causal GQA
+attention over the KV cache ``[B, Hkv, S, D]`` (9943-9946) -> o_proj.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib, ops
+
+
+def rope_tables(head_dim: int, max_pos: int, theta: float, device) -> tuple:
+    """fp32 ``cos``/``sin`` ``[max_pos, head_dim/2]`` with inverse frequencies
+    ``theta^(-2i/D)`` (the first half of the duplicated-half layout)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=device).float() / head_dim))
+    freqs = torch.arange(max_pos, device=device, dtype=torch.float32).unsqueeze(1) * inv_freq
+    return freqs.cos().contiguous(), freqs.sin().contiguous()
+
+
+class KVCache:
+    """Contiguous K/V cache of one layer: ``[B, Hkv, S_max, D]`` bf16 each."""
+
+    def __init__(self, B: int, n_kv: int, S_max: int, head_dim: int, device):
+        self.k = torch.zeros(B, n_kv, S_max, head_dim, dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros_like(self.k)
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[2]
+
+
+class Attention:
+    """One layer's attention.  ``forward`` adds ``o_proj(attn(x))`` to the fp32
+    residual stream in place (the residual add of qwen_with_nki.py:10200 fused
+    into the o_proj epilogue)."""
+
+    def __init__(self, wqkv, q_norm, k_norm, wo, n_q: int, n_kv: int, head_dim: int, eps: float):
+        self.wqkv, self.q_norm, self.k_norm, self.wo = wqkv, q_norm, k_norm, wo
+        self.n_q, self.n_kv, self.head_dim, self.eps = n_q, n_kv, head_dim, eps
+        self.scale = 1.0 / math.sqrt(head_dim)
+        self._ws = {}
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
+                cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start: int = 0,
+                ctx_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``x[B*S, H]`` bf16 (input-normed), ``residual[B*S, H]`` f32 (updated
+        in place), ``positions[B*S]`` i32 (RoPE position == cache index).
+
+        S > 1: causal prefill of a chunk starting at cache index ``start``.
+        S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1).
+        """
+        q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
+                              self.n_q, self.n_kv, cache.k, cache.v, self.eps)
+        if S > 1:
+            o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
+        else:
+            if ctx_len is None:
+                ctx_len = positions + 1
+            ws = self._ws.get((B, cache.capacity))
+            if ws is None:
+                ws = ops.attn_decode_workspace(B, self.n_q, self.head_dim, cache.capacity, x.device)
+                self._ws[(B, cache.capacity)] = ws
+            o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale, ws)
+        ops.gemm(o, self.wo, _lib.GEMM_ADD_F32, out=residual)
+        return residual
