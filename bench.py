@@ -48,7 +48,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=48, help="distinct weight sets rotated through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--extra", action="store_true", help="also time T=8/64 decode and T=4096 prefill")
+    ap.add_argument("--extra", action="store_true",
+                    help="also time T=8/64 decode, T=4096 prefill and the attention layer")
+    ap.add_argument("--model", action="store_true",
+                    help="also time the full 48-layer model (TTFT at 640 tokens, 256 greedy steps)")
     return ap.parse_args()
 
 
@@ -212,6 +215,90 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     }
 
 
+def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
+    """One GQA attention layer (QKV+qk-norm+RoPE, flash attention, o_proj +
+    residual): prefill B x S, then single-token decode steps at the given
+    context lengths (cache capacity 8192 + 1)."""
+    import torch
+
+    from qmoe.attention import Attention, KVCache, rope_tables
+
+    Hq, Hkv, D, Hd = 32, 4, 128, 2048
+    g = torch.Generator(device=dev).manual_seed(4)
+    rnd = lambda *sh: torch.empty(*sh, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=g)
+    one = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    att = Attention(rnd((Hq + 2 * Hkv) * D, Hd), one, one, rnd(Hd, Hq * D), Hq, Hkv, D, 1e-6)
+    cap = max(ctx_points) + 1
+    cache = KVCache(B, Hkv, cap, D, dev)
+    cos, sin = rope_tables(D, cap, 1.0e6, dev)
+    x = torch.randn(B * S, Hd, generator=g, device=dev).to(torch.bfloat16)
+    res = torch.zeros(B * S, Hd, device=dev)
+    pos = torch.arange(S, device=dev, dtype=torch.int32).repeat(B)
+
+    def pre():
+        att.forward(x, res, pos, B, S, cache, cos, sin, 0)
+
+    secs, ev_secs, done = time_graph(pre, 1, reps, 2)
+    flops = 2 * B * S * Hd * (Hq + 2 * Hkv) * D + 2 * B * S * Hq * D * Hd + 2 * 2 * B * Hq * S * S // 2 * D
+    out = {"prefill_us": ev_secs / done * 1e6, "prefill_TFLOPs": flops / (ev_secs / done) / 1e12}
+    xd = torch.randn(B, Hd, generator=g, device=dev).to(torch.bfloat16)
+    rd = torch.zeros(B, Hd, device=dev)
+    for L in ctx_points:
+        pd = torch.full((B,), L - 1, device=dev, dtype=torch.int32)
+        cl = pd + 1
+
+        def dec():
+            att.forward(xd, rd, pd, B, 1, cache, cos, sin, 0, cl)
+
+        secs, ev_secs, done = time_graph(dec, 1, 200, 20)
+        us = ev_secs / done * 1e6
+        byts = ((Hq + 2 * Hkv) * D * Hd + Hd * Hq * D) * 2 + B * Hkv * L * D * 2 * 2
+        out[f"decode_ctx{L}_us"] = us
+        out[f"decode_ctx{L}_GBps"] = byts / (us * 1e-6) / 1e9
+    return out
+
+
+def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
+    """Full Qwen3-30B-A3B-shaped model, random-init bf16, batch 1: TTFT of a
+    640-token prompt of uniform random ids, then greedy decode tokens/s."""
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "nki-moe-7013_amd"))
+    import qwen_with_nki as qn
+
+    nc = qn.MoENeuronConfig(batch_size=1, seq_len=prompt_len + new_tokens, max_length=prompt_len + new_tokens)
+    cfg = qn.Qwen3MoeInferenceConfig(nc)
+    cfg.num_hidden_layers = n_layers
+    m = qn.NeuronQwen3MoeForCausalLM(None, cfg)
+    m.load()
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(0))
+    for _ in range(2):  # warm-up (lazy allocations, graph capture)
+        m.reset()
+        first = m.prefill(prompt).argmax(-1)
+        m.greedy_decode(first, 4)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    m.reset()
+    ev[0].record()
+    first = m.prefill(prompt).argmax(-1)
+    ev[1].record()
+    toks = m.greedy_decode(first, new_tokens)
+    ev[2].record()
+    torch.cuda.synchronize()
+    ttft_ms = ev[0].elapsed_time(ev[1])
+    dec_ms = ev[1].elapsed_time(ev[2])
+    params_b = 61.06e9  # bytes of bf16 weights (30.53 B params)
+    return {
+        "ttft_ms": ttft_ms,
+        "prefill_tokens_per_s": prompt_len / (ttft_ms * 1e-3),
+        "decode_tokens_per_s": new_tokens / (dec_ms * 1e-3),
+        "decode_ms_per_token": dec_ms / new_tokens,
+        "decode_bytes_per_token_GB": 6.083,
+        "decode_GBps": 6.083e9 / (dec_ms / new_tokens * 1e-3) / 1e9,
+        "distinct_tokens": int(torch.unique(toks).numel()),
+    }
+
+
 def cpu_baseline(layer, seconds, dev):
     """fp32 CPU oracle (reference decode schedule, qwen_with_nki.py:3456-3478)
     on one layer's weights: T=1 tokens with fresh random inputs until
@@ -278,6 +365,15 @@ def main():
             print(f"[bench] decode T={T}: {extra[f'decode_T{T}']}", file=sys.stderr, flush=True)
         extra["prefill_T4096"] = bench_prefill(layers, dev)
         print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
+        extra["attention_B8"] = bench_attention(dev)
+        print(f"[bench] attention: {extra['attention_B8']}", file=sys.stderr, flush=True)
+    if a.model:
+        cpu_layer = layers[0]
+        del layers[1:]
+        torch.cuda.empty_cache()
+        extra["model_48L"] = bench_model(dev)
+        print(f"[bench] model: {extra['model_48L']}", file=sys.stderr, flush=True)
+        layers = [cpu_layer]
 
     cpu = None
     if not a.no_cpu_baseline:
