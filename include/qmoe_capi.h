@@ -147,7 +147,8 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed; w2: bf16 [E, H, I];
  *   slot_token/tiles/meta from qmoe_moe_permute with tile_m == 128;
  *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
- *   Limits: H % 128 == 0, I % 64 == 0, 2I % 128 == 0.
+ *   Limits: H % 256 == 0, I % 128 == 0; x, act and one expert's w13 each
+ *   below 2 GiB.
  * Replaces: _nki_cte_moe_left_gate_up_kernel qwen_with_nki.py:5341-5369 (left)
  *   and _nki_cte_moe_down_scatter_kernel 4967-5040 (right), dispatched by
  *   _patched_torch_blockwise_matmul_inference 5872-6003. */
@@ -171,8 +172,9 @@ int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slo
 
 /* Dense GEMM C = A . B^T with an epilogue mode (QMOE_GEMM_*); bf16 inputs,
  * fp32 accumulation.  A: bf16 [M, K] (row stride lda); B: bf16 [N, K];
- * C: [M, N] with row stride ldc.  Limits: K % 64 == 0, N % 128 == 0 when
- * M > 16; K % 512 == 0 when M <= 16 (GEMV path).
+ * C: [M, N] with row stride ldc.  Limits: K % 64 == 0 and A, B below
+ * 2 GiB when M > 16 (MFMA path); K % 512 == 0 when M <= 16 and
+ * M*K <= 32768 (GEMV path).
  * Replaces: the o_proj / lm_head ColumnParallelLinear projections of the
  *   NxDI attention base and model (qwen_with_nki.py:10277-10282);
  *   _nki_lm_head_kernel 1766-1805. */

@@ -5,9 +5,9 @@
 //    staged once in LDS; each wave streams R rows of B with 16-byte
 //    non-temporal loads (K/512 loads per row per lane, all in flight), and
 //    reduces the per-lane partial dots with cross-lane shuffles.
-//  * M > 16: the 128x128 MFMA tile engine (mfma_tile.hpp).
+//  * M > 16: the direct-to-LDS MFMA pipeline (mfma_pipe.hpp).
 #include "gemm.hpp"
-#include "mfma_tile.hpp"
+#include "mfma_pipe.hpp"
 
 namespace qmoe {
 
@@ -77,37 +77,80 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
 }
 
 // ------------------------------------------------------------------ MFMA tile
-template <int MODE>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint16_t* __restrict__ A,
-                                                        int64_t lda,
-                                                        const uint16_t* __restrict__ B, int M,
-                                                        int N, int K, void* __restrict__ C,
-                                                        int64_t ldc) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[tile::SMEM_BYTES / 2];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int m0 = blockIdx.y * tile::BM, n0 = blockIdx.x * tile::BN;
-  const int kc = (t & 7) * 8;
-  const uint16_t* ap[4];
-  const uint16_t* bp[4];
+// Grid = every (row tile, column tile) pair, renumbered XCD-contiguously and
+// then walked in groups of 8 row tiles per column sweep, so the workgroups
+// one XCD runs together share A row panels and B column panels in its L2.
+template <class P, int OCC, int MODE>
+__global__ __launch_bounds__(256, OCC) void gemm_pipe_kernel(const uint16_t* __restrict__ A,
+                                                             int64_t lda,
+                                                             const uint16_t* __restrict__ B,
+                                                             int M, int N, int K,
+                                                             void* __restrict__ C, int64_t ldc) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int gx = (N + P::BN - 1) / P::BN, gy = (M + P::BM - 1) / P::BM;
+  const int item = pipe::xcd_contiguous(int(blockIdx.x), gx * gy);
+  constexpr int GM = 8;
+  const int group = item / (GM * gx), first = group * GM, gm = min(gy - first, GM);
+  const int r = item - group * GM * gx;
+  const int m0 = (first + r % gm) * P::BM, n0 = (r / gm) * P::BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const pipe::i32x4 ra = pipe::make_rsrc(A, uint32_t((int64_t(M) - 1) * lda * 2 + int64_t(K) * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(B, uint32_t(int64_t(N) * K * 2));
+  uint32_t vo[P::NDMA];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = tile::stage_row(t, j);
-    ap[j] = (m0 + r < M) ? A + int64_t(m0 + r) * lda + kc : nullptr;
-    bp[j] = B + int64_t(n0 + r) * K + kc;
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int rr = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(rr, lane);
+    if (j < P::AI)
+      vo[j] = m0 + rr < M ? uint32_t(int64_t(m0 + rr) * lda * 2) + c : pipe::PAD;
+    else
+      vo[j] = n0 + rr < N ? uint32_t(int64_t(n0 + rr) * K * 2) + c : pipe::PAD;
   }
-  tile::Acc acc;
-  tile::mma_128x128(ap, bp, K, smem, acc);
+  typename P::Acc acc;
+  P::run(ra, rb, vo, K / P::BK, smem, acc);
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
+  for (int i = 0; i < P::FM; ++i)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int col = n0 + tile::acc_col(wave, lane, ni);
+    for (int j = 0; j < P::FN; ++j) {
+      const int col = n0 + P::acc_col(wave, j, lane);
+      if (col < N) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m0 + tile::acc_row(wave, lane, mi, i);
-        if (row < M) store_out<MODE>(C, int64_t(row) * ldc + col, acc.c[mi][ni][i]);
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + P::acc_row(wave, i, e, lane);
+          if (row < M) store_out<MODE>(C, int64_t(row) * ldc + col, acc[i][j][e]);
+        }
       }
     }
+}
+
+template <class P, int OCC, int MODE>
+static int launch_pipe(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                       void* C, int64_t ldc, hipStream_t s) {
+  static const bool attr = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_pipe_kernel<P, OCC, MODE>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, P::SMEM);
+    return true;
+  }();
+  (void)attr;
+  const int64_t tiles = int64_t((M + P::BM - 1) / P::BM) * ((N + P::BN - 1) / P::BN);
+  hipLaunchKernelGGL((gemm_pipe_kernel<P, OCC, MODE>), dim3(unsigned(tiles)), dim3(256), P::SMEM, s,
+                     A, lda, B, M, N, K, C, ldc);
+  return hip_status("qmoe_gemm(tile)");
+}
+
+// Tile shape by how many tiles the problem has: 256x256 (one workgroup per
+// CU, least L2 traffic per flop) once it fills the GPU, else smaller tiles
+// with two workgroups per CU.
+template <int MODE>
+static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                       void* C, int64_t ldc, hipStream_t s) {
+  using Big = pipe::Pipe<256, 256, 64, 2>;
+  using Mid = pipe::Pipe<128, 256, 32, 3>;
+  using Small = pipe::Pipe<128, 128, 64, 2>;
+  auto count = [&](int bm, int bn) { return int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (count(256, 256) >= 224) return launch_pipe<Big, 1, MODE>(A, lda, B, M, N, K, C, ldc, s);
+  if (count(128, 256) >= 224) return launch_pipe<Mid, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
+  return launch_pipe<Small, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
 }
 
 // ------------------------------------------------------------------ launcher
@@ -157,23 +200,18 @@ int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, in
         return launch_gemv<QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
     }
   }
-  QMOE_REQUIRE(K % tile::BK == 0, "qmoe_gemm: K %% 64 != 0 (K=%lld)", (long long)K);
-  QMOE_REQUIRE(N % tile::BN == 0, "qmoe_gemm: N %% 128 != 0 (N=%lld)", (long long)N);
-  dim3 grid(N / tile::BN, (M + tile::BM - 1) / tile::BM);
+  QMOE_REQUIRE(K % 64 == 0, "qmoe_gemm: K %% 64 != 0 (K=%lld)", (long long)K);
+  // DMA offsets are 32-bit with the zero-row marker at 2^31
+  QMOE_REQUIRE((M - 1) * lda * 2 + K * 2 < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "qmoe_gemm: A or B larger than 2 GiB");
   switch (mode) {
     case QMOE_GEMM_STORE_BF16:
-      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_STORE_BF16>, grid, dim3(256), 0, s, A, lda, B,
-                         int(M), int(N), int(K), C, ldc);
-      break;
+      return launch_tile<QMOE_GEMM_STORE_BF16>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
     case QMOE_GEMM_STORE_F32:
-      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_STORE_F32>, grid, dim3(256), 0, s, A, lda, B,
-                         int(M), int(N), int(K), C, ldc);
-      break;
+      return launch_tile<QMOE_GEMM_STORE_F32>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
     default:
-      hipLaunchKernelGGL(gemm_tile_kernel<QMOE_GEMM_ADD_F32>, grid, dim3(256), 0, s, A, lda, B,
-                         int(M), int(N), int(K), C, ldc);
+      return launch_tile<QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K), C, ldc, s);
   }
-  return hip_status("qmoe_gemm(tile)");
 }
 
 }  // namespace qmoe

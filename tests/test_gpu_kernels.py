@@ -31,7 +31,9 @@ def _fp32_reference_matmuls():
 
 # --------------------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (5, 4096, 2048), (16, 128, 2048), (8, 2048, 4096),
-                                   (128, 256, 2048), (300, 384, 768), (77, 2048, 4096)])
+                                   (128, 256, 2048), (300, 384, 768), (77, 2048, 4096),
+                                   # ragged N; 128x256 tiles; 256x256 tiles
+                                   (300, 200, 128), (4096, 2048, 1024), (4096, 4096, 256)])
 def test_gemm_vs_fp32(dev, M, N, K):
     announce(f"gemm M={M} N={N} K={K}")
     g = torch.Generator(device=dev).manual_seed(M * 7 + N)
