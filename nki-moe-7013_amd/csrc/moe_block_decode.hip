@@ -1,21 +1,25 @@
 // The whole MoE block at decode shape (T <= 8 tokens) in three launches:
 //
-//   block_router_kernel     [optional post-attention RMSNorm] + router logits:
-//                           ceil(E/4) workgroups, one wave per router row (kept
-//                           in registers); every workgroup normalises the few
-//                           token rows itself, workgroup 0 also stores them.
-//                           The last workgroup to arrive (device-scope counter,
-//                           re-armed by that workgroup) runs softmax/top-k per
-//                           token.  Only ceil(E/4) = 32 workgroups fence, which
-//                           keeps the serialised fence cost to about 2 us.
-//   block_gateup_kernel     the workgroup's active-expert index selects its
-//                           expert from the set of chosen experts (a bitmask
-//                           built from the few top-k ids) and its token rows are
-//                           the (t, j) pairs routed there, so no permutation
-//                           pass is needed.  Gate/up rows are streamed once into
-//                           registers; SwiGLU in fp32: act[t*k+j, i].
-//   block_down_combine_kernel  one workgroup per 4 output columns h (one per
-//                           wave) over all (t, j) pairs: out[t,h] = residual +
+//   block_logits_kernel     [optional post-attention RMSNorm] + router logits:
+//                           E single-wave workgroups, one router row each (in
+//                           registers); every wave normalises the few token
+//                           rows itself, workgroup 0 also stores them.  No
+//                           workgroup waits on another: cross-workgroup
+//                           counters serialise at about 20 ns per workgroup
+//                           on one address, which is what this avoids.
+//   block_gateup_kernel     every workgroup first runs softmax/top-k per token
+//                           on the T*E logits (exact DPP selection, the same
+//                           answer everywhere; workgroup (0,0) publishes it).
+//                           The workgroup's active-expert index then selects
+//                           its expert from the set of chosen experts (a
+//                           bitmask built from the few top-k ids) and its token
+//                           rows are the (t, j) pairs routed there, so no
+//                           permutation pass is needed.  Gate/up rows are
+//                           streamed once into registers; SwiGLU in fp32:
+//                           act[t*k+j, i].
+//   block_down_combine_kernel  one workgroup per 8 output columns h (one per
+//                           wave; 8 waves keep enough loads in flight per CU)
+//                           over all (t, j) pairs: out[t,h] = residual +
 //                           sum_j w[t,j] * act[t*k+j] . W2[e(t,j), h], summed in
 //                           fixed j order (deterministic; no atomics).
 //
@@ -28,107 +32,97 @@ namespace qmoe {
 
 constexpr int BLK_MAX_T = 8;
 constexpr int BLK_MAX_PAIRS = 64;         // T * k
-constexpr int BLK_DOWN_ROWS = 4;          // output columns per down workgroup (1 per wave)
+constexpr int BLK_DOWN_ROWS = 8;          // output columns per down workgroup (1 per wave)
 constexpr int BLK_PAIR_GROUP = 8;         // (t, j) pairs whose W2 rows are loaded together
 constexpr int BLK_ACT_LDS_FLOATS = 8192;  // act staged in LDS when T*k*I fits (32 KB)
 
-// ------------------------------------------------------------------ router + top-k
+// ------------------------------------------------------------------ router logits
+// One wave per router row e.  Each lane owns H/64 positions of the token row
+// (HC chunks of 8 at c*512 + 8*lane), so the optional RMSNorm is a wave
+// reduction over registers: no LDS, no barrier, no cross-workgroup traffic.
+// Workgroup 0 also stores the normalised bf16 rows for the gate/up kernel.
 template <int HC>
-__global__ __launch_bounds__(256) void block_router_kernel(
+__global__ __launch_bounds__(64) void block_logits_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ h, const uint16_t* __restrict__ rms_w,
     float eps, const uint16_t* __restrict__ w_router, const float* __restrict__ bias, int T, int H,
-    int E, int k, float* logits, uint16_t* __restrict__ x_out, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_w, int32_t* sync) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [T][H]
-  __shared__ float red[BLK_MAX_T][4];
-  __shared__ int s_last;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int e = blockIdx.x * 4 + wave;
+    int E, float* __restrict__ logits, uint16_t* __restrict__ x_out) {
+  const int lane = threadIdx.x, e = blockIdx.x;
   u32x4 wr[HC];
-  if (e < E) {
 #pragma unroll
-    for (int c = 0; c < HC; ++c) wr[c] = ld16(w_router + int64_t(e) * H + c * 512 + lane * 8);
-  }
-  if (h) {
-    // fused RMSNorm: pass 1 sums of squares, pass 2 normalise (rows are L2-hot)
-#pragma unroll
-    for (int r = 0; r < BLK_MAX_T; ++r) {
-      if (r < T) {
-        float ss = 0.0f;
-        for (int c = t; c < H / 4; c += 256) {
-          const float4 v = reinterpret_cast<const float4*>(h + int64_t(r) * H)[c];
-          ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) red[r][wave] = ss;
-      }
-    }
-    __syncthreads();
-    for (int r = 0; r < T; ++r) {
-      const float rr = rsqrtf((red[r][0] + red[r][1] + red[r][2] + red[r][3]) / float(H) + eps);
-      for (int c = t; c < H / 4; c += 256) {
-        const float4 v = reinterpret_cast<const float4*>(h + int64_t(r) * H)[c];
-        const uint2 wv = reinterpret_cast<const uint2*>(rms_w)[c];
-        uint2 o;
-        o.x = pack_bf16x2(bf16_lo(wv.x) * (v.x * rr), bf16_hi(wv.x) * (v.y * rr));
-        o.y = pack_bf16x2(bf16_lo(wv.y) * (v.z * rr), bf16_hi(wv.y) * (v.w * rr));
-        reinterpret_cast<uint2*>(xs + r * H)[c] = o;
-        if (blockIdx.x == 0) reinterpret_cast<uint2*>(x_out + int64_t(r) * H)[c] = o;
-      }
-    }
-  } else {
-    stage_rows_bf16(xs, x, nullptr, 0, T, H);
-  }
-  __syncthreads();
-  if (e < E) {
-    const float b = bias ? bias[e] : 0.0f;
-    for (int r = 0; r < T; ++r) {
-      float acc = 0.0f;
+  for (int c = 0; c < HC; ++c) wr[c] = ld_stream(w_router + int64_t(e) * H + c * 512 + lane * 8);
+  const float b = bias ? bias[e] : 0.0f;
+  for (int r = 0; r < T; ++r) {
+    float xf[HC][8];
+    if (h) {
+      float ss = 0.0f;
 #pragma unroll
       for (int c = 0; c < HC; ++c) {
-        opaque(wr[c]);
-        float xf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(xs + r * H + c * 512 + lane * 8), xf);
-        acc += dot8(wr[c], xf);
+        const float4* hp = reinterpret_cast<const float4*>(h + int64_t(r) * H + c * 512 + lane * 8);
+        const float4 v0 = hp[0], v1 = hp[1];
+        xf[c][0] = v0.x; xf[c][1] = v0.y; xf[c][2] = v0.z; xf[c][3] = v0.w;
+        xf[c][4] = v1.x; xf[c][5] = v1.y; xf[c][6] = v1.z; xf[c][7] = v1.w;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) ss += xf[c][q] * xf[c][q];
       }
-      acc = wave_sum(acc);
-      if (lane == 0) logits[int64_t(r) * E + e] = acc + b;
+      const float rr = rsqrtf(wave_sum(ss) / float(H) + eps);
+#pragma unroll
+      for (int c = 0; c < HC; ++c) {
+        float wf[8];
+        unpack8(*reinterpret_cast<const u32x4*>(rms_w + c * 512 + lane * 8), wf);
+        u32x4 o;
+        o.x = pack_bf16x2(wf[0] * (xf[c][0] * rr), wf[1] * (xf[c][1] * rr));
+        o.y = pack_bf16x2(wf[2] * (xf[c][2] * rr), wf[3] * (xf[c][3] * rr));
+        o.z = pack_bf16x2(wf[4] * (xf[c][4] * rr), wf[5] * (xf[c][5] * rr));
+        o.w = pack_bf16x2(wf[6] * (xf[c][6] * rr), wf[7] * (xf[c][7] * rr));
+        unpack8(o, xf[c]);  // the router sees the bf16 normed row, as the experts do
+        if (e == 0) *reinterpret_cast<u32x4*>(x_out + int64_t(r) * H + c * 512 + lane * 8) = o;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < HC; ++c)
+        unpack8(ld16(x + int64_t(r) * H + c * 512 + lane * 8), xf[c]);
     }
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      opaque(wr[c]);
+      acc += dot8(wr[c], xf[c]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[int64_t(r) * E + e] = acc + b;
   }
-  // the last workgroup to arrive selects the experts
-  __threadfence();
-  __syncthreads();
-  if (t == 0) s_last = (atomicAdd(sync, 1) == int(gridDim.x) - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  // stage each token's logits in LDS with vector loads, then rank them there
-  float* s_log = reinterpret_cast<float*>(xs);  // T*E floats <= 8 KB, fits in the x staging area
-  for (int q = t; q < T * E; q += 256) s_log[q] = logits[q];
-  __syncthreads();
-  for (int tok = wave; tok < T; tok += 4)
-    topk_softmax_wave(s_log + tok * E, E, k, topk_idx + tok * k, topk_w + tok * k);
-  if (t == 0) *sync = 0;  // every workgroup has arrived: re-arm
 }
 
 // ------------------------------------------------------------------ gate/up
 template <int HC>
 __global__ __launch_bounds__(256) void block_gateup_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ topk_idx,
+    const uint16_t* __restrict__ x, const float* __restrict__ logits, int E,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     const uint16_t* __restrict__ w13, int T, int H, int I, int k, float* __restrict__ act) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [min(T*k,16)][H]
+  __shared__ float s_log[BLK_MAX_T * ROUTER_MAX_E];
   __shared__ int32_t s_idx[BLK_MAX_PAIRS];
+  __shared__ float s_w[BLK_MAX_PAIRS];
   __shared__ uint32_t s_mask[ROUTER_MAX_E / 32];
   __shared__ int32_t s_list[BLK_MAX_PAIRS];
   __shared__ int s_e, s_n;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int npairs = T * k;
+  // every workgroup selects the experts itself from the T*E logits (same
+  // inputs, same deterministic selection), so no workgroup waits on another
+  for (int q = t; q < T * E; q += 256) s_log[q] = logits[q];
   if (t < ROUTER_MAX_E / 32) s_mask[t] = 0u;
   __syncthreads();
+  for (int tok = wave; tok < T; tok += 4)
+    topk_softmax_wave(s_log + tok * E, E, k, s_idx + tok * k, s_w + tok * k);
+  __syncthreads();
   if (t < npairs) {
-    const int ee = topk_idx[t];
-    s_idx[t] = ee;
+    const int ee = s_idx[t];
     atomicOr(&s_mask[ee >> 5], 1u << (ee & 31));
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      topk_idx[t] = ee;
+      topk_w[t] = s_w[t];
+    }
   }
   __syncthreads();
   if (t == 0) {
@@ -203,7 +197,7 @@ __global__ __launch_bounds__(256) void block_gateup_kernel(
 
 // ------------------------------------------------------------------ down + combine
 template <int IC>
-__global__ __launch_bounds__(256) void block_down_combine_kernel(
+__global__ __launch_bounds__(64 * BLK_DOWN_ROWS) void block_down_combine_kernel(
     const float* __restrict__ act, const uint16_t* __restrict__ w2,
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w,
     const float* residual, int T, int H, int I, int k, float* out) {
@@ -236,7 +230,7 @@ __global__ __launch_bounds__(256) void block_down_combine_kernel(
   }
   const bool act_lds = npairs * I <= BLK_ACT_LDS_FLOATS;
   if (act_lds) {
-    for (int q = t; q < npairs * I / 4; q += 256)
+    for (int q = t; q < npairs * I / 4; q += 64 * BLK_DOWN_ROWS)
       reinterpret_cast<float4*>(s_act)[q] = reinterpret_cast<const float4*>(act)[q];
   }
   __syncthreads();
@@ -282,8 +276,9 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
                                      int64_t E, int64_t k, float* logits, int32_t* topk_idx,
                                      float* topk_w, float* act, int32_t* sync, qmoe_bf16* x_out,
                                      float* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && act && sync && out,
+  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && act && out,
                "qmoe_moe_decode_block: null pointer");
+  (void)sync;  // reserved: the launches no longer synchronise through memory
   QMOE_REQUIRE((x != nullptr) != (h != nullptr), "qmoe_moe_decode_block: pass exactly one of x and h");
   QMOE_REQUIRE(!h || (rms_w && x_out), "qmoe_moe_decode_block: h needs rms_w and x_out");
   QMOE_REQUIRE(T >= 0 && T <= BLK_MAX_T, "qmoe_moe_decode_block: T must be <= 8 (T=%lld)", (long long)T);
@@ -296,19 +291,16 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
   if (T == 0) return QMOE_OK;
   hipStream_t s = as_stream(stream);
   const uint16_t* xin = h ? x_out : x;
-  const size_t shm0 = std::max<size_t>(size_t(T) * H * 2, size_t(T) * E * 4);
-  dim3 g0(unsigned((E + 3) / 4));
   const size_t shm1 = size_t(std::min<int64_t>(T * k, DEC_TOK_CHUNK)) * H * 2;
   dim3 g1(unsigned(std::min<int64_t>(E, T * k)), unsigned(I / 8));
   switch (H / 512) {
 #define QMOE_BLK(HC)                                                                              \
   case HC:                                                                                        \
-    hipLaunchKernelGGL(block_router_kernel<HC>, g0, dim3(256), shm0, s, x, h, rms_w, eps,         \
-                       w_router, bias, int(T), int(H), int(E), int(k), logits, x_out, topk_idx,   \
-                       topk_w, sync);                                                             \
+    hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(64), 0, s, x, h, rms_w,    \
+                       eps, w_router, bias, int(T), int(H), int(E), logits, x_out);               \
     if (int rc = hip_status("qmoe_moe_decode_block(router)")) return rc;                          \
-    hipLaunchKernelGGL(block_gateup_kernel<HC>, g1, dim3(256), shm1, s, xin, topk_idx, w13,       \
-                       int(T), int(H), int(I), int(k), act);                                      \
+    hipLaunchKernelGGL(block_gateup_kernel<HC>, g1, dim3(256), shm1, s, xin, logits, int(E),      \
+                       topk_idx, topk_w, w13, int(T), int(H), int(I), int(k), act);               \
     break;
     QMOE_BLK(1)
     QMOE_BLK(2)
@@ -321,8 +313,8 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
   switch (int((I / 8 + 63) / 64)) {
 #define QMOE_DC(IC)                                                                               \
   case IC:                                                                                        \
-    hipLaunchKernelGGL(block_down_combine_kernel<IC>, g2, dim3(256), 0, s, act, w2, topk_idx,      \
-                       topk_w, residual, int(T), int(H), int(I), int(k), out);                    \
+    hipLaunchKernelGGL(block_down_combine_kernel<IC>, g2, dim3(64 * BLK_DOWN_ROWS), 0, s, act, w2, \
+                       topk_idx, topk_w, residual, int(T), int(H), int(I), int(k), out);          \
     break;
     QMOE_DC(1)
     QMOE_DC(2)
