@@ -15,44 +15,52 @@ constexpr int ROUTER_MAX_K = 16;
 
 // Selection by k rounds of wave-wide reductions over order-preserving 32-bit
 // keys (the monotone bit pattern of the logit): a DPP max finds the largest
-// remaining logit, a DPP min the lowest expert index holding it (ties go to
-// the lower index); the owner lane records the rank and clears the key.  No
-// LDS traffic.
+// remaining logit, a second DPP max over complemented indices the lowest
+// expert index holding it (ties go to the lower index); the owner lane
+// records the rank and clears the key.  No LDS traffic.
 // The weights use the exact logits: exp(l - l_max) / sum over the chosen k.
 // lr: the token's E logits (bias already added if any); may point to LDS.
 // Writes every slot of out_idx[0..k) / out_w[0..k) (NaN logits rank as -inf).
-template <bool MAX>
-__device__ __forceinline__ uint32_t dpp_reduce_u32_wave(uint32_t v) {
-#define QMOE_RED(CTRL, RM)                                                                     \
-  {                                                                                            \
-    const uint32_t o = uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), CTRL, RM, 0xf, false)); \
-    v = MAX ? max(v, o) : min(v, o);                                                           \
-  }
-  QMOE_RED(QMOE_DPP_ROW_SHR(1), 0xf)
-  QMOE_RED(QMOE_DPP_ROW_SHR(2), 0xf)
-  QMOE_RED(QMOE_DPP_ROW_SHR(4), 0xf)
-  QMOE_RED(QMOE_DPP_ROW_SHR(8), 0xf)
-  QMOE_RED(QMOE_DPP_ROW_BCAST15, 0xa)
-  QMOE_RED(QMOE_DPP_ROW_BCAST31, 0xc)
-#undef QMOE_RED
+// Wave-wide unsigned max, lane 63's value broadcast.  Each step is one
+// v_max_u32_dpp in place: row_shr with bound_ctrl reads 0 (the identity)
+// past a row's start, and the masked row_bcast steps leave the other rows'
+// value as it is.  DPP reads a VGPR that the previous VALU op wrote, which
+// needs two wait states: the s_nop 1 between steps (and before the first).
+// Every lane of the wave must be active.
+__device__ __forceinline__ uint32_t dpp_max_u32_wave(uint32_t v) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(v));
   return uint32_t(__builtin_amdgcn_readlane(int(v), 63));
 }
 
-__device__ __forceinline__ void topk_softmax_wave(const float* lr, int E, int k, int32_t* out_idx,
-                                                  float* out_w) {
-  constexpr int J = ROUTER_MAX_E / 64;
+// J = keys per lane (E <= 64*J); topk_softmax_wave picks the smallest J.
+template <int J>
+__device__ __forceinline__ void topk_softmax_wave_j(const float* lr, int E, int k, int32_t* out_idx,
+                                                    float* out_w) {
   const int lane = threadIdx.x & 63;
   float v[J];
   uint32_t key[J];
   int rank[J];
-  float m = -INFINITY;
+  uint32_t top = 0u;  // round 0's key: the largest logit
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int e = lane + 64 * j;
-    float l = (e < E) ? lr[e] : -INFINITY;
-    l = (l != l) ? -INFINITY : l;
+    float l = lr[min(e, E - 1)];  // unconditional, so the J loads issue together
+    l = (e >= E || l != l) ? -INFINITY : l;
     v[j] = l;
-    m = fmaxf(m, l);
     const uint32_t b = __float_as_uint(l);
     const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     key[j] = (e < E) ? ord : 0u;  // valid keys are >= ord(-inf) = 0x007fffff
@@ -64,12 +72,14 @@ __device__ __forceinline__ void topk_softmax_wave(const float* lr, int E, int k,
       uint32_t best = key[0];
 #pragma unroll
       for (int j = 1; j < J; ++j) best = max(best, key[j]);
-      best = dpp_reduce_u32_wave<true>(best);
-      uint32_t cand = 0xffffffffu;
+      best = dpp_max_u32_wave(best);
+      if (r == 0) top = best;
+      // lowest index holding `best`: a max over complemented indices
+      uint32_t cand = 0u;
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        if (key[j] == best) cand = min(cand, uint32_t(lane + 64 * j));
-      const uint32_t win = dpp_reduce_u32_wave<false>(cand);
+        if (key[j] == best) cand = max(cand, ~uint32_t(lane + 64 * j));
+      const uint32_t win = ~dpp_max_u32_wave(cand);
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         if (uint32_t(lane + 64 * j) == win) {
@@ -79,7 +89,7 @@ __device__ __forceinline__ void topk_softmax_wave(const float* lr, int E, int k,
       }
     }
   }
-  m = wave_max(m);
+  const float m = __uint_as_float((top & 0x80000000u) ? (top & 0x7fffffffu) : ~top);
   float p[J];
   float s = 0.0f;
 #pragma unroll
@@ -96,6 +106,17 @@ __device__ __forceinline__ void topk_softmax_wave(const float* lr, int E, int k,
       out_w[rank[j]] = p[j] * inv;
     }
   }
+}
+
+__device__ __forceinline__ void topk_softmax_wave(const float* lr, int E, int k, int32_t* out_idx,
+                                                  float* out_w) {
+  static_assert(ROUTER_MAX_E == 256, "dispatch below covers E <= 256");
+  if (E <= 64)
+    topk_softmax_wave_j<1>(lr, E, k, out_idx, out_w);
+  else if (E <= 128)
+    topk_softmax_wave_j<2>(lr, E, k, out_idx, out_w);
+  else
+    topk_softmax_wave_j<4>(lr, E, k, out_idx, out_w);
 }
 
 }  // namespace qmoe

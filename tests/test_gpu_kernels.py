@@ -426,9 +426,17 @@ def test_moe_decode_block(dev, experts, router_w, T, normed):
     outs = [run(residual, None) for _ in range(3)]
     inplace = residual.clone()
     run(inplace, inplace)
+    # a different input on the same workspace gives the fresh-workspace result
+    x2 = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    second = ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x2, residual=residual, bufs=bufs)
+    fresh = ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x2, residual=residual,
+                                 bufs=ops.DecodeBlockBuffers.alloc(T, H, I, E, K_TOP, dev))
     torch.cuda.synchronize()
+    assert torch.equal(second, fresh)
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     assert torch.equal(outs[0], inplace)
+    outs[0] = run(residual, None)  # restore bufs (logits, top-k) for the checks below
+    torch.cuda.synchronize()
     if normed:  # the fused RMSNorm output: one bf16 rounding of the fp32 value
         err = (bufs.x_out.float().cpu() - oracle.rmsnorm(h.cpu(), rms_w.cpu(), 1e-6)).abs()
         assert float((err - x_ref.float().abs() * 2 ** -8).max()) <= 1e-5
