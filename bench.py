@@ -71,7 +71,7 @@ def make_layers(n_layers, dev, seed=0):
     for _ in range(n_layers):
         w_router = torch.empty(E, H, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
         w13 = torch.empty(E, 2 * I, H, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
-        w2 = torch.empty(E, H, I, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
+        w2 = torch.empty(E, I // 8, H, 8, device=dev, dtype=torch.bfloat16).normal_(0.0, 0.02, generator=g)
         layers.append((w_router, w13, w2))
     return layers
 
@@ -315,7 +315,7 @@ def cpu_baseline(layer, seconds, dev):
     gate_up = torch.empty(E, H, 2 * I)
     for e0 in range(0, E, 16):  # unpack on the GPU in slices, then upcast on the host
         gate_up[e0 : e0 + 16] = weights.unpack_gate_up(w13[e0 : e0 + 16]).float().cpu()
-    down = w2.transpose(1, 2).float().cpu().contiguous()  # (E, I, H)
+    down = weights.unpack_down(w2).float().cpu()  # (E, I, H)
     g = torch.Generator().manual_seed(0)
     n = 0
     for _ in range(3):  # warm-up

@@ -45,6 +45,15 @@ typedef void* qmoe_stream_t;
  * [64j, 64j+32) are gate rows [32j, 32j+32), the next 32 the matching up rows. */
 #define QMOE_W13_GROUP 32
 
+/* Blocked layout of the down weight: w2 is bf16 [E][I/8][H][8], element
+ * (e, ib, h, ii) = W2[e][h][8*ib + ii] (W2[e] = the [H, I] down matrix).  An
+ * 8-unit slice of one expert's down matrix is one contiguous H x 16-byte run. */
+#define QMOE_W2_BLOCK 8
+
+/* Workgroups of the decode block's expert kernel (one per MI355X CU); sets
+ * the size of its partial-output workspace. */
+#define QMOE_DECODE_BLOCK_WGS 256
+
 int qmoe_version(void);
 const char* qmoe_last_error(void);
 
@@ -100,20 +109,21 @@ int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* b
                    int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
 
 /* The whole MoE block at decode shape (T <= 8) in three launches: router
- * logits + top-k (with the post-attention RMSNorm fused when h is given),
- * gate/up GEMV (each workgroup picks its expert from the chosen set; no
- * permutation pass), and the down GEMV with the weighted combine and
- * residual add:
+ * logits (with the post-attention RMSNorm fused when h is given); the expert
+ * kernel (top-k in every workgroup, then work items of one touched expert and
+ * 8 intermediate units each: gate/up rows, SwiGLU, and the matching down
+ * block, accumulated into a per-workgroup partial output); and a fixed-order
+ * reduction of the partials with the residual add:
  *   xin = x, or bf16(rmsnorm(h) * rms_w) written to x_out
  *   out[t] = residual[t] + sum_j topk_w[t,j] * expert_{topk_idx[t,j]}(xin[t])
  *   x: bf16 [T,H] or NULL; h: f32 [T,H] or NULL (exactly one of x, h);
  *   rms_w: bf16 [H] and x_out: bf16 [T,H] (with h); w_router: bf16 [E,H];
- *   bias: f32 [E] or NULL; w13: bf16 [E,2I,H] packed; w2: bf16 [E,H,I];
- *   residual: f32 [T,H] or NULL (may alias out and h); outputs logits f32
- *   [T,E], topk_idx i32 [T,k], topk_w f32 [T,k]; act: f32 [T*k, I] workspace;
- *   sync: i32 [1] arrival counter, 0 before the first call and left 0 (calls
- *   sharing it must not overlap); out: f32 [T,H].  The combine sums
- *   j = 0..k-1 in order (deterministic).
+ *   bias: f32 [E] or NULL; w13: bf16 [E,2I,H] packed (QMOE_W13_GROUP);
+ *   w2: bf16 [E, I/8, H, 8] blocked (QMOE_W2_BLOCK); residual: f32 [T,H] or
+ *   NULL (may alias out and h); outputs logits f32 [T,E], topk_idx i32 [T,k],
+ *   topk_w f32 [T,k]; workspace: device memory of at least
+ *   qmoe_moe_decode_block_workspace(T, H) bytes (calls sharing it must not
+ *   overlap); out: f32 [T,H].  Deterministic: every sum runs in a fixed order.
  *   Limits: T <= 8, T*k <= 64, E <= 256, k <= 16, H in {512, 1024, 2048,
  *   4096}, I % 32 == 0, I <= 1536.
  * Replaces: the decode MoE path of NeuronQwen3MoeDecoderLayer.forward
@@ -124,13 +134,20 @@ int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* r
                           const qmoe_bf16* w_router, const float* bias, const qmoe_bf16* w13,
                           const qmoe_bf16* w2, const float* residual, int64_t T, int64_t H,
                           int64_t I, int64_t E, int64_t k, float* logits, int32_t* topk_idx,
-                          float* topk_w, float* act, int32_t* sync, qmoe_bf16* x_out, float* out,
-                          qmoe_stream_t stream);
+                          float* topk_w, void* workspace, int64_t workspace_bytes,
+                          qmoe_bf16* x_out, float* out, qmoe_stream_t stream);
+
+/* Workspace bytes qmoe_moe_decode_block needs for T tokens of width H
+ * (QMOE_DECODE_BLOCK_WGS * T * H floats); -1 for negative sizes.
+ * Replaces: nothing in the reference (its kernels allocate their own HBM
+ *   scratch, e.g. qwen_with_nki.py:1858); the caller owns memory here. */
+int64_t qmoe_moe_decode_block_workspace(int64_t T, int64_t H);
 
 /* Decode expert MLPs without the combine (bandwidth-bound GEMV form; each
  * touched expert's weights are streamed once for all tokens routed to it).
  *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed (QMOE_W13_GROUP);
- *   w2: bf16 [E, H, I]; offsets/slot_token/active/meta from qmoe_moe_permute;
+ *   w2: bf16 [E, I/8, H, 8] blocked (QMOE_W2_BLOCK); offsets/slot_token/active/meta
+ *   from qmoe_moe_permute;
  *   act: f32 [T*k, I] workspace; y_slot: f32 [T*k, H] unweighted expert outputs.
  *   Limits: T <= 64, H in {512, 1024, 2048, 4096}, I % 32 == 0, I <= 1536.
  * Replaces: ExpertMLPsV2.forward_selective_loading (decode), restated at
@@ -144,7 +161,7 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
 /* Prefill expert MLPs as two grouped GEMMs on bf16 MFMA:
  *   act[s]    = bf16(silu(x[tok(s)] . Wg[e]^T) * (x[tok(s)] . Wu[e]^T))
  *   y_slot[s] = bf16(act[s] . W2[e]^T)
- *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed; w2: bf16 [E, H, I];
+ *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed; w2: bf16 [E, I/8, H, 8] blocked;
  *   slot_token/tiles/meta from qmoe_moe_permute with tile_m == 128;
  *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
  *   Limits: H % 256 == 0, I % 128 == 0; x, act and one expert's w13 each

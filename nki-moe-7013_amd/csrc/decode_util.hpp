@@ -7,7 +7,7 @@ namespace qmoe {
 
 constexpr int DEC_TOK_CHUNK = 16;  // token rows staged in LDS at a time
 constexpr int DEC_MAX_T = 64;
-constexpr int DOWN_ROWS_PER_WG = 32;
+constexpr int DOWN_NB = 16;  // w2 blocks per register batch of the down GEMV
 
 // Keeps a register value opaque to the optimiser inside a loop, so that
 // loop-invariant conversions of it are not hoisted (hoisting the bf16 -> fp32

@@ -104,11 +104,12 @@ struct Pipe {
 
   // acc = A_tile . B_tile^T over nk stages of BK.  vo[j] = source byte offset
   // of DMA instruction j for this lane at k = 0 (PAD for a zero row); the k
-  // advance goes in soffset.  Ends with every wave past its last LDS read
-  // only after the caller's next barrier, so callers that reuse smem must
-  // __syncthreads() first.
+  // advance goes in soffset: BK*2 bytes per stage for A, b_step for B (BK*2
+  // for a K-contiguous B; other values for blocked B layouts).  Ends with
+  // every wave past its last LDS read only after the caller's next barrier,
+  // so callers that reuse smem must __syncthreads() first.
   __device__ static void run(i32x4 ra, i32x4 rb, const uint32_t (&vo)[NDMA], int nk, uint8_t* smem,
-                             Acc& acc) {
+                             Acc& acc, uint32_t b_step = uint32_t(BK * 2)) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
@@ -119,14 +120,14 @@ struct Pipe {
 
     auto dma_part = [&](int kt, int part) {
       const uint32_t sb = lds0 + uint32_t((kt % S) * STAGE);
-      const uint32_t soff = uint32_t(kt * BK * 2);
+      const uint32_t soff_a = uint32_t(kt * BK * 2), soff_b = uint32_t(kt) * b_step;
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
         const int j = part * PER + q;
         if (j < AI)
-          dma16(sb + uint32_t((wave * AI + j) * 1024), vo[j], ra, soff);
+          dma16(sb + uint32_t((wave * AI + j) * 1024), vo[j], ra, soff_a);
         else
-          dma16(sb + uint32_t(A_BYTES + (wave * BI + (j - AI)) * 1024), vo[j], rb, soff);
+          dma16(sb + uint32_t(A_BYTES + (wave * BI + (j - AI)) * 1024), vo[j], rb, soff_b);
       }
     };
 #pragma unroll

@@ -7,40 +7,47 @@
 //                           workgroup waits on another: cross-workgroup
 //                           counters serialise at about 20 ns per workgroup
 //                           on one address, which is what this avoids.
-//   block_gateup_kernel     every workgroup first runs softmax/top-k per token
-//                           on the T*E logits (exact DPP selection, the same
-//                           answer everywhere; workgroup (0,0) publishes it).
-//                           The workgroup's active-expert index then selects
-//                           its expert from the set of chosen experts (a
-//                           bitmask built from the few top-k ids) and its token
-//                           rows are the (t, j) pairs routed there, so no
-//                           permutation pass is needed.  Gate/up rows are
-//                           streamed once into registers; SwiGLU in fp32:
-//                           act[t*k+j, i].
-//   block_down_combine_kernel  one workgroup per 8 output columns h (one per
-//                           wave; 8 waves keep enough loads in flight per CU)
-//                           over all (t, j) pairs: out[t,h] = residual +
-//                           sum_j w[t,j] * act[t*k+j] . W2[e(t,j), h], summed in
-//                           fixed j order (deterministic; no atomics).
+//   block_expert_kernel     BLK_WGS workgroups.  Each first runs softmax/top-k
+//                           per token on the T*E logits (exact DPP selection,
+//                           the same answer everywhere; workgroup 0 publishes
+//                           it) and lists the touched experts in ascending id.
+//                           The work items are (touched expert u, slice s of
+//                           BLK_SLICE intermediate units); workgroup g takes
+//                           items g, g + BLK_WGS, ...  An item streams the
+//                           slice's gate and up rows (2 * 8 rows of H) and the
+//                           expert's down block w2[e][s] (H x 8, contiguous in
+//                           the blocked layout) once, computes the 8 SwiGLU
+//                           outputs per routed token (times the routing
+//                           weight), and adds their down product to the
+//                           workgroup's running partial output in registers.
+//                           The next item's weights are in flight while the
+//                           current one is computed.  No workgroup waits on
+//                           another: the gate/up -> down dependency stays
+//                           inside the item.
+//   block_reduce_kernel     out[t,h] = residual[t,h] + sum_g partial[g][t][h],
+//                           g in a fixed order (deterministic; no atomics).
 //
 // HBM traffic is the touched experts' weights (U * 3 * H * I * 2 bytes) plus
-// the router (E * H * 2); everything else is a few KB.
+// the router (E * H * 2); the partials are BLK_WGS * T * H * 4 bytes (2 MB at
+// T = 1), written once and read once.
 #include "decode_util.hpp"
 #include "topk_impl.hpp"
 
 namespace qmoe {
 
 constexpr int BLK_MAX_T = 8;
-constexpr int BLK_MAX_PAIRS = 64;         // T * k
-constexpr int BLK_DOWN_ROWS = 8;          // output columns per down workgroup (1 per wave)
-constexpr int BLK_PAIR_GROUP = 8;         // (t, j) pairs whose W2 rows are loaded together
-constexpr int BLK_ACT_LDS_FLOATS = 8192;  // act staged in LDS when T*k*I fits (32 KB)
+constexpr int BLK_MAX_PAIRS = 64;  // T * k
+constexpr int BLK_SLICE = QMOE_W2_BLOCK;  // intermediate units per work item
+constexpr int BLK_WGS = QMOE_DECODE_BLOCK_WGS;
+constexpr int BLK_RED_WAVES = 8;
+
+static_assert(BLK_SLICE == 8, "an item is 4 waves x 2 units");
 
 // ------------------------------------------------------------------ router logits
 // One wave per router row e.  Each lane owns H/64 positions of the token row
 // (HC chunks of 8 at c*512 + 8*lane), so the optional RMSNorm is a wave
 // reduction over registers: no LDS, no barrier, no cross-workgroup traffic.
-// Workgroup 0 also stores the normalised bf16 rows for the gate/up kernel.
+// Workgroup 0 also stores the normalised bf16 rows for the expert kernel.
 template <int HC>
 __global__ __launch_bounds__(64) void block_logits_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ h, const uint16_t* __restrict__ rms_w,
@@ -93,192 +100,299 @@ __global__ __launch_bounds__(64) void block_logits_kernel(
   }
 }
 
-// ------------------------------------------------------------------ gate/up
+// ------------------------------------------------------------------ experts
+// Weights of one work item held by one thread: gate rows i, i+1 and up rows
+// i, i+1 (i = s*8 + 2*wave) as HC 16-byte chunks each (lane*8 + c*512), and
+// DQ = H/256 down rows h = tid + 256*q, 8 bf16 (the slice) each.
 template <int HC>
-__global__ __launch_bounds__(256) void block_gateup_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ logits, int E,
-    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
-    const uint16_t* __restrict__ w13, int T, int H, int I, int k, float* __restrict__ act) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [min(T*k,16)][H]
+struct ItemRegs {
+  u32x4 g[4][HC];
+  u32x4 d[2 * HC];
+};
+
+// GR item groups of 4 waves per workgroup; group r of workgroup g takes
+// items g*GR + r, then + gridDim.x*GR, ...  PF: the next item's loads are
+// issued before the current item is computed (two register sets).
+template <int HC, int MT, int GR, bool PF>
+__global__ __launch_bounds__(256 * GR) void block_expert_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ logits, int E, int k,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, const uint16_t* __restrict__ w13,
+    const uint16_t* __restrict__ w2b, int T, int H, int I, float* __restrict__ partial) {
+  constexpr int DQ = 2 * HC;  // H / 256
+  constexpr int NT = 256 * GR;
+  // dynamic LDS: x rows [T][H] bf16, then (GR > 1) the group-combine buffer [T][H] f32
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];
   __shared__ float s_log[BLK_MAX_T * ROUTER_MAX_E];
   __shared__ int32_t s_idx[BLK_MAX_PAIRS];
   __shared__ float s_w[BLK_MAX_PAIRS];
-  __shared__ uint32_t s_mask[ROUTER_MAX_E / 32];
-  __shared__ int32_t s_list[BLK_MAX_PAIRS];
-  __shared__ int s_e, s_n;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int npairs = T * k;
-  // every workgroup selects the experts itself from the T*E logits (same
-  // inputs, same deterministic selection), so no workgroup waits on another
-  for (int q = t; q < T * E; q += 256) s_log[q] = logits[q];
-  if (t < ROUTER_MAX_E / 32) s_mask[t] = 0u;
+  __shared__ float s_wt[ROUTER_MAX_E][BLK_MAX_T];  // routing weight of (e, t) where routed
+  __shared__ uint32_t s_tm[ROUTER_MAX_E];          // bit t: token t is routed to expert e
+  __shared__ int32_t s_uexp[ROUTER_MAX_E];         // touched experts, ascending
+  __shared__ int s_wcnt[4];
+  __shared__ __attribute__((aligned(16))) float s_act[GR][2][MT][BLK_SLICE];
+  const int tid = threadIdx.x, grp = tid >> 8, gt = tid & 255, lane = tid & 63, wave = gt >> 6;
+  float* s_red = reinterpret_cast<float*>(s_x + T * H);
+
+  for (int q = tid; q < T * E; q += NT) s_log[q] = logits[q];
+  for (int q = tid; q < E; q += NT) s_tm[q] = 0u;
+  for (int q = tid; q < T * H / 8; q += NT)
+    reinterpret_cast<u32x4*>(s_x)[q] = ld16(x + int64_t(q) * 8);
   __syncthreads();
-  for (int tok = wave; tok < T; tok += 4)
-    topk_softmax_wave(s_log + tok * E, E, k, s_idx + tok * k, s_w + tok * k);
+  for (int t = tid >> 6; t < T; t += NT / 64)
+    topk_softmax_wave(s_log + t * E, E, k, s_idx + t * k, s_w + t * k);
   __syncthreads();
-  if (t < npairs) {
-    const int ee = s_idx[t];
-    atomicOr(&s_mask[ee >> 5], 1u << (ee & 31));
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-      topk_idx[t] = ee;
-      topk_w[t] = s_w[t];
+  if (tid < T * k) {
+    const int e = s_idx[tid], t = tid / k;
+    atomicOr(&s_tm[e], 1u << t);
+    s_wt[e][t] = s_w[tid];
+    if (blockIdx.x == 0) {
+      topk_idx[tid] = e;
+      topk_w[tid] = s_w[tid];
     }
   }
   __syncthreads();
-  if (t == 0) {
-    int a = blockIdx.x, ex = -1;
-    for (int wd = 0; wd < ROUTER_MAX_E / 32 && ex < 0; ++wd) {
-      uint32_t m = s_mask[wd];
-      const int c = __popc(m);
-      if (a < c) {
-        for (int q = 0; q < a; ++q) m &= m - 1;  // drop the a lowest set bits
-        ex = wd * 32 + __ffs(m) - 1;
-      } else {
-        a -= c;
-      }
-    }
-    s_e = ex;
+  // compact the touched experts in ascending id (E <= 256: waves 0-3, one
+  // thread per expert id)
+  const bool used = tid < E && s_tm[tid] != 0u;
+  const unsigned long long used_m = __ballot(used);
+  if (tid < 256 && lane == 0) s_wcnt[wave] = __popcll(used_m);
+  __syncthreads();
+  if (used) {
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += s_wcnt[w];
+    s_uexp[base + __popcll(used_m & ((1ull << lane) - 1ull))] = tid;
   }
   __syncthreads();
-  const int e = s_e;
-  if (e < 0) return;
-  const int i_base = blockIdx.y * 8 + wave * 2;
-  const int grp = i_base / 32, off = i_base % 32;
-  const uint16_t* we = w13 + int64_t(e) * 2 * I * H;
-  u32x4 w[4][HC];  // gate i_base, gate i_base+1, up i_base, up i_base+1
+  const int U = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+  const int NS = I / BLK_SLICE;
+  const int n_items = U * NS;
+  const int stride = int(gridDim.x) * GR;
+
+  float part[MT][DQ];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int prow = grp * 64 + (r < 2 ? 0 : 32) + off + (r & 1);
-    const uint16_t* p = we + int64_t(prow) * H + lane * 8;
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int c = 0; c < HC; ++c) w[r][c] = ld_stream(p + c * 512);
-  }
-  if (wave == 0) {
-    const bool hit = lane < npairs && s_idx[lane] == e;
-    const unsigned long long m = __ballot(hit);
-    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    if (hit) s_list[__popcll(m & lt)] = lane;
-    if (lane == 0) s_n = __popcll(m);
-  }
-  __syncthreads();
-  const int n_all = s_n;
-  for (int c0 = 0; c0 < n_all; c0 += DEC_TOK_CHUNK) {
-    const int n = min(DEC_TOK_CHUNK, n_all - c0);
-    if (c0 > 0) __syncthreads();
-    const int hch = H / 8;
-    for (int q = t; q < n * hch; q += 256) {
-      const int j = q / hch, kc = q - j * hch;
-      const int64_t row = s_list[c0 + j] / k;
-      *reinterpret_cast<u32x4*>(xs + j * H + kc * 8) = ld16(x + row * H + kc * 8);
+    for (int q = 0; q < DQ; ++q) part[t][q] = 0.0f;
+
+  auto load = [&](int it, ItemRegs<HC>& r) {
+    const int u = it / NS, s = it - u * NS;
+    const int e = s_uexp[u];
+    const int i0 = s * BLK_SLICE + 2 * wave;  // this wave's two units (same 32-group)
+    const uint16_t* we = w13 + int64_t(e) * 2 * I * H;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int prow = (i0 / QMOE_W13_GROUP) * 2 * QMOE_W13_GROUP + (q < 2 ? 0 : QMOE_W13_GROUP) +
+                       (i0 % QMOE_W13_GROUP) + (q & 1);
+      const uint16_t* p = we + int64_t(prow) * H + lane * 8;
+#pragma unroll
+      for (int c = 0; c < HC; ++c) r.g[q][c] = ld_stream(p + c * 512);
     }
-    __syncthreads();
-    for (int j = 0; j < n; ++j) {
-      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint16_t* wd = w2b + (int64_t(e) * NS + s) * H * BLK_SLICE + gt * BLK_SLICE;
 #pragma unroll
-      for (int c = 0; c < HC; ++c) {
-        float xf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(xs + j * H + c * 512 + lane * 8), xf);
+    for (int q = 0; q < DQ; ++q) r.d[q] = ld_stream(wd + q * 256 * BLK_SLICE);
+  };
+
+  // One named barrier per group would be ideal; the whole workgroup's
+  // barrier is used instead, so every group runs the same number of
+  // compute steps (n_steps below) and idle groups still reach it.
+  auto compute = [&](int it, ItemRegs<HC>& r, int buf, bool live) {
+    const int e = live ? s_uexp[it / NS] : 0;
+    const uint32_t tm = live ? s_tm[e] : 0u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          opaque(w[r][c]);
-          acc[r] += dot8(w[r][c], xf);
+    for (int t = 0; t < MT; ++t) {
+      if (t < T && ((tm >> t) & 1u)) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < HC; ++c) {
+          float xf[8];
+          unpack8(*reinterpret_cast<const u32x4*>(s_x + t * H + c * 512 + lane * 8), xf);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            opaque(r.g[q][c]);
+            acc[q] += dot8(r.g[q][c], xf);
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = wave_sum(acc[q]);
+        if (lane == 0) {
+          const float wt = s_wt[e][t];
+          s_act[grp][buf][t][2 * wave] = silu(acc[0]) * acc[2] * wt;
+          s_act[grp][buf][t][2 * wave + 1] = silu(acc[1]) * acc[3] * wt;
         }
       }
+    }
+    __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane < 2) {
-        const float g = lane ? acc[1] : acc[0];
-        const float u = lane ? acc[3] : acc[2];
-        act[int64_t(s_list[c0 + j]) * I + i_base + lane] = silu(g) * u;
+    for (int t = 0; t < MT; ++t) {
+      if (t < T && ((tm >> t) & 1u)) {
+        const float4 a0 = *reinterpret_cast<const float4*>(&s_act[grp][buf][t][0]);
+        const float4 a1 = *reinterpret_cast<const float4*>(&s_act[grp][buf][t][4]);
+        const float a8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) {
+          opaque(r.d[q]);
+          part[t][q] += dot8(r.d[q], a8);
+        }
       }
     }
+    // Every register of the item counts as consumed here, on every path:
+    // otherwise the refill two items later waits (WAW) on loads issued after
+    // these, which serialises the stream.
+    if (live) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int c = 0; c < HC; ++c) opaque(r.g[q][c]);
+#pragma unroll
+      for (int q = 0; q < DQ; ++q) opaque(r.d[q]);
+    }
+  };
+
+  // items of this group: first, first + stride, ...; all groups loop n_steps
+  // times (the most any group has) so the workgroup barriers match up.
+  const int first = int(blockIdx.x) * GR + grp;
+  const int first0 = int(blockIdx.x) * GR;  // group 0 has the most items
+  const int n_steps = first0 < n_items ? (n_items - first0 + stride - 1) / stride : 0;
+  ItemRegs<HC> ra;
+  if constexpr (PF) {
+    ItemRegs<HC> rb;
+    int it = first;
+    if (it < n_items) load(it, ra);
+    for (int st = 0; st < n_steps; st += 2) {
+      const int it2 = it + stride;
+      if (it2 < n_items) load(it2, rb);
+      compute(it, ra, 0, it < n_items);
+      if (st + 1 >= n_steps) break;
+      const int it3 = it2 + stride;
+      if (it3 < n_items) load(it3, ra);
+      compute(it2, rb, 1, it2 < n_items);
+      it = it3;
+    }
+  } else {
+    int it = first;
+    for (int st = 0; st < n_steps; ++st, it += stride) {
+      if (it < n_items) load(it, ra);
+      compute(it, ra, st & 1, it < n_items);
+    }
+  }
+
+  // combine the groups in a fixed order (group 0 + 1 + 2 ...), then store
+  if constexpr (GR > 1) {
+    for (int r = 1; r < GR; ++r) {
+      if (grp == r) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          if (t < T)
+#pragma unroll
+            for (int q = 0; q < DQ; ++q) s_red[t * H + q * 256 + gt] = part[t][q];
+      }
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          if (t < T)
+#pragma unroll
+            for (int q = 0; q < DQ; ++q) part[t][q] += s_red[t * H + q * 256 + gt];
+      }
+      __syncthreads();
+    }
+  }
+  if (grp == 0) {
+    float* pp = partial + int64_t(blockIdx.x) * T * H + gt;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      if (t < T)
+#pragma unroll
+        for (int q = 0; q < DQ; ++q) pp[t * H + q * 256] = part[t][q];
   }
 }
 
-// ------------------------------------------------------------------ down + combine
-template <int IC>
-__global__ __launch_bounds__(64 * BLK_DOWN_ROWS) void block_down_combine_kernel(
-    const float* __restrict__ act, const uint16_t* __restrict__ w2,
-    const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w,
-    const float* residual, int T, int H, int I, int k, float* out) {
-  __shared__ int32_t s_idx[BLK_MAX_PAIRS];
-  __shared__ float s_w[BLK_MAX_PAIRS];
-  __shared__ __attribute__((aligned(16))) float s_act[BLK_ACT_LDS_FLOATS];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int npairs = T * k;
-  const int hrow = blockIdx.x * BLK_DOWN_ROWS + wave;
-  const int ichunks = I / 8;
-  // first group's W2 rows go out before anything else (expert ids read directly)
-  u32x4 w[BLK_PAIR_GROUP][IC];
-  auto load_group = [&](int p0) {
+// ------------------------------------------------------------------ reduce
+// One workgroup per (64 columns, token): wave w sums partials g = w, w + 8,
+// ... in order; the 8 wave sums are added in wave order.
+// All BLK_WGS / BLK_RED_WAVES loads of a lane are issued before the first add.
+__global__ __launch_bounds__(64 * BLK_RED_WAVES) void block_reduce_kernel(
+    const float* __restrict__ partial, const float* residual, int T, int H, float* out) {
+  constexpr int PER = BLK_WGS / BLK_RED_WAVES;
+  static_assert(PER * BLK_RED_WAVES == BLK_WGS, "partials per wave");
+  __shared__ float s_sum[BLK_RED_WAVES][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane, t = blockIdx.y;
+  const float* p = partial + int64_t(t) * H + h;
+  const int64_t stride = int64_t(T) * H;
+  float v[PER];
 #pragma unroll
-    for (int g = 0; g < BLK_PAIR_GROUP; ++g) {
-      const int p = p0 + g;
-      const int e = p < npairs ? topk_idx[p] : 0;
-      const uint16_t* rowp = w2 + (int64_t(e) * H + hrow) * I;
+  for (int q = 0; q < PER; ++q) v[q] = p[int64_t(wave + q * BLK_RED_WAVES) * stride];
+  float acc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < IC; ++c) {
-        const int ch = lane + 64 * c;
-        w[g][c] = (p < npairs && ch < ichunks) ? ld_stream(rowp + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  load_group(0);
-  if (t < npairs) {
-    s_idx[t] = topk_idx[t];
-    s_w[t] = topk_w[t];
-  }
-  const bool act_lds = npairs * I <= BLK_ACT_LDS_FLOATS;
-  if (act_lds) {
-    for (int q = t; q < npairs * I / 4; q += 64 * BLK_DOWN_ROWS)
-      reinterpret_cast<float4*>(s_act)[q] = reinterpret_cast<const float4*>(act)[q];
-  }
+  for (int q = 0; q < PER; ++q) acc += v[q];
+  s_sum[wave][lane] = acc;
   __syncthreads();
-  float run = 0.0f;  // running weighted sum of the current token (wave-uniform)
-  for (int p0 = 0; p0 < npairs; p0 += BLK_PAIR_GROUP) {
-    if (p0 > 0) load_group(p0);
+  if (wave == 0) {
+    float v = s_sum[0][lane];
 #pragma unroll
-    for (int g = 0; g < BLK_PAIR_GROUP; ++g) {
-      const int p = p0 + g;
-      if (p < npairs) {
-        const float* ap = act_lds ? s_act + p * I : act + int64_t(p) * I;
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < IC; ++c) {
-          const int ch = lane + 64 * c;
-          if (ch < ichunks) {
-            const float4 a0 = reinterpret_cast<const float4*>(ap + ch * 8)[0];
-            const float4 a1 = reinterpret_cast<const float4*>(ap + ch * 8)[1];
-            const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            acc += dot8(w[g][c], x8);
-          }
-        }
-        acc = wave_sum(acc);
-        const int j = p % k;
-        run = (j == 0) ? s_w[p] * acc : fmaf(s_w[p], acc, run);
-        if (j == k - 1 && lane == 0) {
-          const int64_t o = int64_t(p / k) * H + hrow;
-          out[o] = (residual ? residual[o] : 0.0f) + run;
-        }
-      }
-    }
+    for (int w = 1; w < BLK_RED_WAVES; ++w) v += s_sum[w][lane];
+    const int64_t o = int64_t(t) * H + h;
+    out[o] = (residual ? residual[o] : 0.0f) + v;
   }
+}
+
+}  // namespace qmoe
+
+namespace qmoe {
+
+template <int HC, int MT, int GR, bool PF>
+static void launch_expert_cfg(const uint16_t* x, const float* logits, int64_t E, int64_t k,
+                              int32_t* topk_idx, float* topk_w, const uint16_t* w13,
+                              const uint16_t* w2b, int64_t T, int64_t H, int64_t I, float* partial,
+                              hipStream_t s) {
+  auto fn = block_expert_kernel<HC, MT, GR, PF>;
+  const size_t shm = size_t(T) * H * 2 + (GR > 1 ? size_t(T) * H * 4 : 0);
+  static const bool attr = [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    return true;
+  }();
+  (void)attr;
+  hipLaunchKernelGGL(fn, dim3(BLK_WGS), dim3(256 * GR), shm, s, x, logits, int(E), int(k), topk_idx,
+                     topk_w, w13, w2b, int(T), int(H), int(I), partial);
+}
+
+// T = 1: three item groups per workgroup (12 waves per CU; at the MoE shape
+// every group gets exactly one item, so the whole 76 MB is requested at once).
+// T <= 8: register budget of the 8-token accumulators allows two groups
+// (one for H = 4096).
+template <int HC>
+static void launch_block_experts(const uint16_t* x, const float* logits, int64_t E, int64_t k,
+                                 int32_t* topk_idx, float* topk_w, const uint16_t* w13,
+                                 const uint16_t* w2b, int64_t T, int64_t H, int64_t I,
+                                 float* partial, hipStream_t s) {
+  if (T == 1)
+    launch_expert_cfg<HC, 1, (HC <= 4 ? 3 : 1), (HC > 4)>(x, logits, E, k, topk_idx, topk_w, w13,
+                                                          w2b, T, H, I, partial, s);
+  else
+    launch_expert_cfg<HC, BLK_MAX_T, (HC <= 4 ? 2 : 1), false>(x, logits, E, k, topk_idx, topk_w,
+                                                               w13, w2b, T, H, I, partial, s);
 }
 
 }  // namespace qmoe
 
 using namespace qmoe;
 
+extern "C" int64_t qmoe_moe_decode_block_workspace(int64_t T, int64_t H) {
+  if (T < 0 || H < 0) return -1;
+  return int64_t(BLK_WGS) * T * H * int64_t(sizeof(float));
+}
+
 extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* rms_w,
                                      float eps, const qmoe_bf16* w_router, const float* bias,
                                      const qmoe_bf16* w13, const qmoe_bf16* w2,
                                      const float* residual, int64_t T, int64_t H, int64_t I,
                                      int64_t E, int64_t k, float* logits, int32_t* topk_idx,
-                                     float* topk_w, float* act, int32_t* sync, qmoe_bf16* x_out,
-                                     float* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && act && out,
+                                     float* topk_w, void* workspace, int64_t workspace_bytes,
+                                     qmoe_bf16* x_out, float* out, qmoe_stream_t stream) {
+  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && workspace && out,
                "qmoe_moe_decode_block: null pointer");
-  (void)sync;  // reserved: the launches no longer synchronise through memory
   QMOE_REQUIRE((x != nullptr) != (h != nullptr), "qmoe_moe_decode_block: pass exactly one of x and h");
   QMOE_REQUIRE(!h || (rms_w && x_out), "qmoe_moe_decode_block: h needs rms_w and x_out");
   QMOE_REQUIRE(T >= 0 && T <= BLK_MAX_T, "qmoe_moe_decode_block: T must be <= 8 (T=%lld)", (long long)T);
@@ -286,21 +400,23 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
                "qmoe_moe_decode_block: need E <= 256, k <= min(16, E), T*k <= 64");
   QMOE_REQUIRE(H >= 512 && H <= 4096 && H % 512 == 0 && (H / 512 & (H / 512 - 1)) == 0,
                "qmoe_moe_decode_block: H must be 512, 1024, 2048 or 4096");
-  QMOE_REQUIRE(I % 32 == 0 && I > 0 && I <= 1536, "qmoe_moe_decode_block: I must be a multiple of 32, <= 1536");
+  QMOE_REQUIRE(I % QMOE_W13_GROUP == 0 && I > 0 && I <= 1536,
+               "qmoe_moe_decode_block: I must be a multiple of 32, <= 1536");
   QMOE_REQUIRE(eps >= 0.0f, "qmoe_moe_decode_block: eps < 0");
+  QMOE_REQUIRE(workspace_bytes >= qmoe_moe_decode_block_workspace(T, H),
+               "qmoe_moe_decode_block: workspace of %lld bytes < %lld", (long long)workspace_bytes,
+               (long long)qmoe_moe_decode_block_workspace(T, H));
   if (T == 0) return QMOE_OK;
   hipStream_t s = as_stream(stream);
   const uint16_t* xin = h ? x_out : x;
-  const size_t shm1 = size_t(std::min<int64_t>(T * k, DEC_TOK_CHUNK)) * H * 2;
-  dim3 g1(unsigned(std::min<int64_t>(E, T * k)), unsigned(I / 8));
+  float* partial = static_cast<float*>(workspace);
   switch (H / 512) {
 #define QMOE_BLK(HC)                                                                              \
   case HC:                                                                                        \
     hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(64), 0, s, x, h, rms_w,    \
                        eps, w_router, bias, int(T), int(H), int(E), logits, x_out);               \
     if (int rc = hip_status("qmoe_moe_decode_block(router)")) return rc;                          \
-    hipLaunchKernelGGL(block_gateup_kernel<HC>, g1, dim3(256), shm1, s, xin, logits, int(E),      \
-                       topk_idx, topk_w, w13, int(T), int(H), int(I), int(k), act);               \
+    launch_block_experts<HC>(xin, logits, E, k, topk_idx, topk_w, w13, w2, T, H, I, partial, s);  \
     break;
     QMOE_BLK(1)
     QMOE_BLK(2)
@@ -308,18 +424,8 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
     QMOE_BLK(8)
 #undef QMOE_BLK
   }
-  if (int rc = hip_status("qmoe_moe_decode_block(gate_up)")) return rc;
-  dim3 g2(unsigned(H / BLK_DOWN_ROWS));
-  switch (int((I / 8 + 63) / 64)) {
-#define QMOE_DC(IC)                                                                               \
-  case IC:                                                                                        \
-    hipLaunchKernelGGL(block_down_combine_kernel<IC>, g2, dim3(64 * BLK_DOWN_ROWS), 0, s, act, w2, \
-                       topk_idx, topk_w, residual, int(T), int(H), int(I), int(k), out);          \
-    break;
-    QMOE_DC(1)
-    QMOE_DC(2)
-    QMOE_DC(3)
-#undef QMOE_DC
-  }
-  return hip_status("qmoe_moe_decode_block(down)");
+  if (int rc = hip_status("qmoe_moe_decode_block(experts)")) return rc;
+  hipLaunchKernelGGL(block_reduce_kernel, dim3(unsigned(H / 64), unsigned(T)), dim3(64 * BLK_RED_WAVES),
+                     0, s, partial, residual, int(T), int(H), out);
+  return hip_status("qmoe_moe_decode_block(reduce)");
 }

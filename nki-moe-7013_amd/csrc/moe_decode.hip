@@ -4,7 +4,8 @@
 //   moe_gateup_gemv_kernel   act[s,i] = silu(x.Wg[e,i]) * (x.Wu[e,i]) (fp32).
 //                            The expert's gate/up rows go into registers and are
 //                            applied to the expert's (few) token rows staged in LDS.
-//   moe_down_gemv_kernel     y_slot[s,h] = act[s].W2[e,h] (fp32).
+//   moe_down_gemv_kernel     y_slot[s,h] = act[s].W2[e,h] (fp32), from the blocked
+//                            w2 layout [E][I/8][H][8] (one column per thread).
 //
 // Grid: (active-expert slot, row group); slots beyond the number of touched
 // experts (meta[1]) exit at once, so the host sizes the grid as min(E, T*k)
@@ -70,30 +71,26 @@ __global__ __launch_bounds__(256) void moe_gateup_gemv_kernel(
   }
 }
 
-// ================================================================== down (+ combine)
-template <int IC>
+// ================================================================== down
+// Workgroup: (active-expert slot, 256 output columns).  Thread t owns column
+// h = 256*blockIdx.y + t and walks the expert's I/8 blocks of the blocked w2
+// ([I/8][H][8]): each 16-byte load is that column's 8 weights of one block,
+// so a wave's load is 1 KB contiguous and no cross-lane reduction is needed.
+// DOWN_NB blocks are loaded per batch; the expert's token rows (act, f32) are
+// staged in LDS DEC_TOK_CHUNK at a time.
+template <int NB>
 __global__ __launch_bounds__(256) void moe_down_gemv_kernel(
-    const float* __restrict__ act, const uint16_t* __restrict__ w2,
+    const float* __restrict__ act, const uint16_t* __restrict__ w2b,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ active,
     const int32_t* __restrict__ meta, int H, int I, float* __restrict__ y_slot) {
   extern __shared__ __attribute__((aligned(16))) float as[];  // [DEC_TOK_CHUNK][I]
   if (int(blockIdx.x) >= meta[1]) return;
   const int e = active[blockIdx.x];
   const int s0 = offsets[e], s1 = offsets[e + 1];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int h_base = blockIdx.y * DOWN_ROWS_PER_WG + wave * 8;
-  const int ichunks = I / 8;
-  const uint16_t* we = w2 + int64_t(e) * H * I;
-  u32x4 w[8][IC];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const uint16_t* p = we + int64_t(h_base + r) * I;
-#pragma unroll
-    for (int c = 0; c < IC; ++c) {
-      const int ch = lane + 64 * c;
-      w[r][c] = (ch < ichunks) ? ld_stream(p + ch * 8) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
+  const int t = threadIdx.x;
+  const int h = blockIdx.y * 256 + t;
+  const int NS = I / QMOE_W2_BLOCK;
+  const uint16_t* wp = w2b + (int64_t(e) * NS * H + h) * QMOE_W2_BLOCK;
   for (int c0 = s0; c0 < s1; c0 += DEC_TOK_CHUNK) {
     const int n = min(DEC_TOK_CHUNK, s1 - c0);
     __syncthreads();
@@ -104,34 +101,33 @@ __global__ __launch_bounds__(256) void moe_down_gemv_kernel(
           reinterpret_cast<const float4*>(act + int64_t(c0 + j) * I)[c];
     }
     __syncthreads();
-    for (int j = 0; j < n; ++j) {
-      float acc[8];
+    float acc[DEC_TOK_CHUNK];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) acc[r] = 0.0f;
+    for (int j = 0; j < DEC_TOK_CHUNK; ++j) acc[j] = 0.0f;
+    for (int b0 = 0; b0 < NS; b0 += NB) {
+      u32x4 w[NB];
 #pragma unroll
-      for (int c = 0; c < IC; ++c) {
-        const int ch = lane + 64 * c;
-        if (ch < ichunks) {
-          const float4 a0 = reinterpret_cast<const float4*>(as + j * I + ch * 8)[0];
-          const float4 a1 = reinterpret_cast<const float4*>(as + j * I + ch * 8)[1];
-          const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      for (int b = 0; b < NB; ++b)
+        w[b] = (b0 + b < NS) ? ld_stream(wp + int64_t(b0 + b) * H * QMOE_W2_BLOCK) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            opaque(w[r][c]);
-            acc[r] += dot8(w[r][c], x8);
+      for (int j = 0; j < DEC_TOK_CHUNK; ++j) {
+        if (j < n) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            if (b0 + b < NS) {
+              const float4 a0 = reinterpret_cast<const float4*>(as + j * I + (b0 + b) * 8)[0];
+              const float4 a1 = reinterpret_cast<const float4*>(as + j * I + (b0 + b) * 8)[1];
+              const float x8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+              opaque(w[b]);
+              acc[j] += dot8(w[b], x8);
+            }
           }
         }
       }
-#pragma unroll
-      for (int r = 0; r < 8; ++r) acc[r] = wave_sum(acc[r]);
-      if (lane < 8) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < 8; ++r)
-          if (lane == r) v = acc[r];
-        y_slot[int64_t(c0 + j) * H + h_base + lane] = v;
-      }
     }
+#pragma unroll
+    for (int j = 0; j < DEC_TOK_CHUNK; ++j)
+      if (j < n) y_slot[int64_t(c0 + j) * H + h] = acc[j];
   }
 }
 
@@ -169,20 +165,9 @@ static int launch_experts(const uint16_t* x, const uint16_t* w13, const uint16_t
   int rc = hip_status("moe experts (gate_up)");
   if (rc) return rc;
   const size_t shm2 = size_t(stage_rows) * I * 4;
-  dim3 g2(nact, unsigned(H / DOWN_ROWS_PER_WG));
-  switch (int((I / 8 + 63) / 64)) {
-#define QMOE_DN(IC)                                                                             \
-  case IC:                                                                                      \
-    hipLaunchKernelGGL(moe_down_gemv_kernel<IC>, g2, dim3(256), shm2, s, act, w2, offsets,      \
-                       active, meta, int(H), int(I), y_slot);                                   \
-    break;
-    QMOE_DN(1)
-    QMOE_DN(2)
-    QMOE_DN(3)
-#undef QMOE_DN
-    default:
-      return fail(QMOE_ERR_INVALID, "moe experts: unsupported I=%lld", (long long)I);
-  }
+  dim3 g2(nact, unsigned(H / 256));
+  hipLaunchKernelGGL(moe_down_gemv_kernel<DOWN_NB>, g2, dim3(256), shm2, s, act, w2, offsets, active,
+                     meta, int(H), int(I), y_slot);
   return hip_status("moe experts (down)");
 }
 

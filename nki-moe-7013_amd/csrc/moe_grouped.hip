@@ -14,7 +14,10 @@
 //             (gate, up) in the same lane and register: the SwiGLU epilogue
 //             act = bf16(silu(g) * u) is elementwise, fp32 before the cast.
 //   down:     A rows = act[s] (already contiguous in slot order),
-//             B = 256 rows of w2[e]; the epilogue writes y_slot[s] in bf16.
+//             B = 256 rows h of w2[e] in the blocked layout [I/8][H][8]: the
+//             16-byte chunk (h, k..k+7) sits at ((k/8)*H + h)*16, so a stage
+//             of BK = 32 columns is 4 chunks of every row, BK/8*H*16 bytes
+//             further on per stage; the epilogue writes y_slot[s] in bf16.
 //
 // Grid: one workgroup per (tile, column tile) up to max_tiles; the live ones
 // (tile < meta[0]) are renumbered XCD-contiguously, column tiles fastest, so
@@ -26,6 +29,7 @@ namespace qmoe {
 
 namespace {
 using GP = pipe::Pipe<128, 256, 32, 3>;
+static_assert(GP::BK % QMOE_W2_BLOCK == 0, "a stage covers whole w2 blocks");
 
 struct TileJob {
   int e, s0, rows, n0;
@@ -102,11 +106,11 @@ __global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(
     const uint32_t c = GP::dma_chunk(r, lane);
     if (j < GP::AI)
       vo[j] = r < job.rows ? uint32_t(job.s0 + r) * uint32_t(I * 2) + c : pipe::PAD;
-    else
-      vo[j] = uint32_t(job.n0 + r) * uint32_t(I * 2) + c;
+    else  // chunk index c/16 of this stage = k block; rows h contiguous within a block
+      vo[j] = ((c / 16) * uint32_t(H) + uint32_t(job.n0 + r)) * 16u;
   }
   GP::Acc acc;
-  GP::run(ra, rb, vo, I / GP::BK, smem, acc);
+  GP::run(ra, rb, vo, I / GP::BK, smem, acc, uint32_t(GP::BK / QMOE_W2_BLOCK) * uint32_t(H) * 16u);
 #pragma unroll
   for (int i = 0; i < GP::FM; ++i)
 #pragma unroll

@@ -20,6 +20,8 @@ GEMM_STORE_F32 = 1
 GEMM_ADD_F32 = 2
 
 W13_GROUP = 32
+W2_BLOCK = 8
+DECODE_BLOCK_WGS = 256
 
 P = c_void_p
 I64 = c_int64
@@ -33,7 +35,8 @@ PROTOTYPES = {
     "qmoe_moe_permute": (c_int, [P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
     "qmoe_moe_route": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "qmoe_moe_decode_block": (
-        c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
+        c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, P, P, P]),
+    "qmoe_moe_decode_block_workspace": (c_int64, [I64, I64]),
     "qmoe_moe_experts_gemv": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_experts_grouped": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_combine": (c_int, [P, c_int, P, P, P, I64, I64, I64, P, P]),

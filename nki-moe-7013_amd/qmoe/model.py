@@ -227,7 +227,7 @@ def random_params(config: Qwen3MoeInferenceConfig, device, seed: int = 0, std: f
             "input_layernorm": ones(H), "post_attention_layernorm": ones(H),
             "wqkv": rnd((nq + 2 * nkv) * D, H), "q_norm": ones(D), "k_norm": ones(D),
             "wo": rnd(H, nq * D), "router": rnd(E, H),
-            "w13": rnd(E, 2 * I, H), "w2": rnd(E, H, I),
+            "w13": rnd(E, 2 * I, H), "w2": rnd(E, I // 8, H, 8),
         })
     return {"embed_tokens": rnd(c.vocab_size, H), "layers": layers, "norm": ones(H),
             "lm_head": rnd(c.vocab_size, H)}
@@ -241,7 +241,7 @@ def convert_qwen3_moe_hf_to_neuron_state_dict(state_dict: Dict[str, torch.Tensor
     (qwen_with_nki.py:8883-8997): q/k/v concatenated (8845-8862), q_norm/k_norm,
     router from ``mlp.gate.weight`` (8915-8919), per-expert gate/up/down packed
     (8928-8990) -- here into the gate/up-interleaved ``w13 [E,2I,H]`` and
-    ``w2 [E,H,I]`` layouts.  Accepts keys with or without the ``model.`` prefix.
+    blocked ``w2 [E,I/8,H,8]`` layouts.  Accepts keys with or without the ``model.`` prefix.
     """
     sd = {k[len("model."):] if k.startswith("model.") else k: v for k, v in state_dict.items()}
     bf = lambda t: t.to(torch.bfloat16).contiguous()

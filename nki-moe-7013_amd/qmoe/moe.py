@@ -27,7 +27,7 @@ TILE_M = 128
 
 
 class ExpertMLPs:
-    """Routed SwiGLU experts with packed weights ``w13 [E,2I,H]``, ``w2 [E,H,I]``."""
+    """Routed SwiGLU experts with packed weights ``w13 [E,2I,H]`` and blocked ``w2 [E,I/8,H,8]``."""
 
     def __init__(self, w13: torch.Tensor, w2: torch.Tensor, top_k: int,
                  normalize_top_k_affinities: bool = True):

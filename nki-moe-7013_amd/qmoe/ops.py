@@ -201,8 +201,14 @@ def _check_experts(x, w13, w2):
     if H2 != H or I2 % 2:
         raise ValueError(f"w13 must be [E, 2I, H={H}] (got {tuple(w13.shape)})")
     I = I2 // 2
-    _need(w2, "w2", BF16, (E, H, I))
+    _need_w2(w2, E, H, I)
     return T, H, I, E
+
+
+def _need_w2(w2, E, H, I):
+    if I % _lib.W2_BLOCK:
+        raise ValueError(f"moe intermediate size {I} is not a multiple of {_lib.W2_BLOCK}")
+    _need(w2, "w2 (blocked [E, I/8, H, 8])", BF16, (E, I // _lib.W2_BLOCK, H, _lib.W2_BLOCK))
 
 
 def moe_experts_gemv(
@@ -237,16 +243,17 @@ class DecodeBlockBuffers:
     logits: torch.Tensor  # [T, E] f32
     topk_idx: torch.Tensor  # [T, k] i32
     topk_w: torch.Tensor  # [T, k] f32
-    act: torch.Tensor  # [T*k, I] f32
+    workspace: torch.Tensor  # u8, qmoe_moe_decode_block_workspace(T, H) bytes
     x_out: torch.Tensor  # [T, H] bf16 (normalised input, when h is given)
-    sync: torch.Tensor  # [1] i32 arrival counter (zero at rest)
 
     @staticmethod
     def alloc(T: int, H: int, I: int, E: int, k: int, device) -> "DecodeBlockBuffers":
+        nbytes = int(lib().qmoe_moe_decode_block_workspace(T, H))
         return DecodeBlockBuffers(
             torch.empty(T, E, dtype=F32, device=device), torch.empty(T, k, dtype=I32, device=device),
-            torch.empty(T, k, dtype=F32, device=device), torch.empty(T * k, I, dtype=F32, device=device),
-            torch.empty(T, H, dtype=BF16, device=device), torch.zeros(1, dtype=I32, device=device))
+            torch.empty(T, k, dtype=F32, device=device),
+            torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device),
+            torch.empty(T, H, dtype=BF16, device=device))
 
 
 DECODE_BLOCK_MAX_T = 8
@@ -259,7 +266,9 @@ def moe_decode_block(
     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
     bufs: Optional[DecodeBlockBuffers] = None,
 ) -> torch.Tensor:
-    """Whole decode MoE block (T <= 8) in three launches:
+    """Whole decode MoE block (T <= 8) in three launches (router logits;
+    top-k + fused gate/up/down work items with per-workgroup partial outputs;
+    fixed-order reduction + residual):
     ``out = residual + MoE(x)`` with ``x`` given, or ``x = rmsnorm(h) * rms_w``."""
     if (x is None) == (h is None):
         raise ValueError("pass exactly one of x (bf16) and h (f32)")
@@ -278,7 +287,7 @@ def moe_decode_block(
     if w13.shape[0] != E or w13.shape[2] != H:
         raise ValueError("w13 must be [E, 2I, H]")
     I = w13.shape[1] // 2
-    _need(w2, "w2", BF16, (E, H, I))
+    _need_w2(w2, E, H, I)
     if bias is not None:
         _need(bias, "bias", F32, (E,))
     if residual is not None:
@@ -288,16 +297,16 @@ def moe_decode_block(
     _need(bufs.logits, "logits", F32, (T, E))
     _need(bufs.topk_idx, "topk_idx", I32, (T, k))
     _need(bufs.topk_w, "topk_w", F32, (T, k))
-    _need(bufs.act, "act", F32, (T * k, I))
+    _need(bufs.workspace, "workspace", torch.uint8)
     _need(bufs.x_out, "x_out", BF16, (T, H))
     out = torch.empty(T, H, dtype=F32, device=dev) if out is None else out
     _need(out, "out", F32, (T, H))
-    _same_device(src, w_router, w13, w2, bias, residual, out, bufs.act)
+    _same_device(src, w_router, w13, w2, bias, residual, out, bufs.workspace)
     check(
         lib().qmoe_moe_decode_block(
             _ptr(x), _ptr(h), _ptr(rms_w), float(eps), _ptr(w_router), _ptr(bias), _ptr(w13), _ptr(w2),
             _ptr(residual), T, H, I, E, k, _ptr(bufs.logits), _ptr(bufs.topk_idx), _ptr(bufs.topk_w),
-            _ptr(bufs.act), _ptr(bufs.sync), _ptr(bufs.x_out), _ptr(out), _stream(),
+            _ptr(bufs.workspace), bufs.workspace.numel(), _ptr(bufs.x_out), _ptr(out), _stream(),
         ),
         "qmoe_moe_decode_block",
     )

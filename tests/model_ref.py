@@ -25,13 +25,14 @@ def layer_weights_f32(lw, experts=True):
         "q_norm": lw["q_norm"].float(), "k_norm": lw["k_norm"].float(),
         "router": lw["router"].float(),
         "gate_up_proj": weights.unpack_gate_up(lw["w13"]).float() if experts else None,
-        "down_proj": lw["w2"].transpose(1, 2).float() if experts else None,
+        "down_proj": weights.unpack_down(lw["w2"]).float() if experts else None,
     }
 
 
 def expert_f32(lw, e):
     """One expert's NxDI-layout fp32 weights: gate_up (H, 2I), down (I, H)."""
-    return weights.unpack_gate_up(lw["w13"][e : e + 1]).float()[0], lw["w2"][e].float().t()
+    return (weights.unpack_gate_up(lw["w13"][e : e + 1]).float()[0],
+            weights.unpack_down(lw["w2"][e : e + 1]).float()[0])
 
 
 def cfg_dict(config):

@@ -52,6 +52,16 @@ def test_version():
         (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2048, 100, 128, 8, 1, 1, None), "I % 128"),
         (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2176, 768, 128, 8, 1, 1, None), "H % 256"),
         (lambda l: l.qmoe_moe_combine(1, 0, 1, 1, None, 4, 8, 6, 1, None), "H % 4"),
+        # decode block: x, h, rms_w, eps, w_router, bias, w13, w2, residual, T, H, I, E, k,
+        #   logits, topk_idx, topk_w, workspace, workspace_bytes, x_out, out, stream
+        (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 768, 128, 8,
+                                           1, 1, 1, 1, 256 * 2048 * 4 - 4, None, 1, None), "workspace"),
+        (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 9, 2048, 768, 128, 8,
+                                           1, 1, 1, 1, 1 << 30, None, 1, None), "T must be"),
+        (lambda l: l.qmoe_moe_decode_block(1, 1, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 768, 128, 8,
+                                           1, 1, 1, 1, 1 << 30, None, 1, None), "exactly one"),
+        (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 100, 128, 8,
+                                           1, 1, 1, 1, 1 << 30, None, 1, None), "multiple of 32"),
         (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 1, 1, 2048, 32, 4, 64, 10, 1e-6, 1, 1, 1, None), "head_dim"),
         (lambda l: l.qmoe_attn_prefill(1, 1, 1, 1, 10, 32, 4, 128, 8, 0, 0.1, 1, None), "S_max"),
         (lambda l: l.qmoe_attn_decode(1, 1, 1, 1, 1, 64, 2, 128, 16, 0.1, 1, 1, None), "Hq / Hkv <= 16"),
@@ -82,6 +92,36 @@ def test_check_maps_status_to_exceptions():
     with pytest.raises(_lib.QmoeError):
         _lib.check(_lib.QMOE_ERR_HIP, "x")
     _lib.check(_lib.QMOE_OK, "x")
+
+
+def test_decode_block_workspace_size():
+    lib = _lib.lib()
+    assert lib.qmoe_moe_decode_block_workspace(1, 2048) == _lib.DECODE_BLOCK_WGS * 2048 * 4
+    assert lib.qmoe_moe_decode_block_workspace(8, 512) == _lib.DECODE_BLOCK_WGS * 8 * 512 * 4
+    assert lib.qmoe_moe_decode_block_workspace(-1, 2048) == -1
+
+
+def test_blocked_down_layout():
+    """w2[e, b, h, j] = down[e, 8b + j, h] (NxDI (E, I, H)) = W2[e, h, 8b + j];
+    both conversions invert, and the HF path lands on the same bytes."""
+    g = torch.Generator().manual_seed(3)
+    E, I, H = 3, 40, 24
+    down = torch.randn(E, I, H, generator=g)  # NxDI (E, I, H)
+    b = weights.pack_down(down)
+    assert tuple(b.shape) == (E, I // 8, H, 8)
+    for e, blk, h, j in [(0, 0, 0, 0), (1, 2, 5, 7), (2, 4, 23, 3), (0, 3, 11, 1)]:
+        assert b[e, blk, h, j] == down[e, 8 * blk + j, h]
+    assert torch.equal(weights.unpack_down(b), down)
+    w_ehi = down.transpose(1, 2).contiguous()  # (E, H, I)
+    assert torch.equal(weights.block_down(w_ehi), b)
+    assert torch.equal(weights.unblock_down(b), w_ehi)
+    # one 8-unit slice of one expert is a contiguous H x 8 run
+    flat = b.reshape(-1)
+    s = 2
+    assert torch.equal(flat[(1 * (I // 8) + s) * H * 8 : (1 * (I // 8) + s + 1) * H * 8].view(H, 8),
+                       down[1, 8 * s : 8 * s + 8, :].t())
+    with pytest.raises(ValueError):
+        weights.block_down(torch.zeros(1, 4, 12))
 
 
 def test_pack_gate_up_roundtrip_and_layout():

@@ -170,7 +170,7 @@ def test_permute_rejects_out_of_range_ids(dev):
 def experts(dev):
     g = torch.Generator(device=dev).manual_seed(2024)
     w13 = bf16_randn((E, 2 * I, H), g, dev, std=0.02)
-    w2 = bf16_randn((E, H, I), g, dev, std=0.02)
+    w2 = bf16_randn((E, I // 8, H, 8), g, dev, std=0.02)  # blocked layout (random values)
     return w13, w2
 
 
@@ -183,7 +183,7 @@ class _ExpertCache:
     def __getitem__(self, e):
         if e not in self.c:
             gu = weights.unpack_gate_up(self.w13[e : e + 1]).float().cpu()[0]  # (H, 2I)
-            dn = self.w2[e].float().cpu().t().contiguous()  # (I, H)
+            dn = weights.unpack_down(self.w2[e : e + 1]).float().cpu()[0]  # (I, H)
             self.c[e] = (gu, dn)
         return self.c[e]
 
