@@ -9,11 +9,16 @@ the residual add) on the next layer's weights; the 48-call rotation is
 captured once in a HIP graph and replayed.
 
 Prints ONE JSON line.  ``value`` is MoE-block tokens/s (T tokens per step).
-``roofline`` is for the dominant kernel(s): the decode expert GEMV pair
-(gate_up + down, one ``qmoe_moe_experts_gemv`` call), timed with HIP events on
-the stream it runs on, against its algorithmic bytes U * 9,437,184 (U =
-distinct experts touched, measured).  ``cpu_baseline`` is the fp32 CPU oracle
-(the reference's decode schedule) on a bounded sample of the same workload.
+``roofline`` is for the decode block (one ``qmoe_moe_decode_block`` call:
+router logits, fused expert items, reduce), timed with HIP events on the
+stream the graph replays on, against its algorithmic bytes
+U * 9,437,184 + 524,288 (U = distinct experts touched, measured).
+``roofline.traffic`` is the HBM-side bytes per call measured live with two
+``rocprofv3 --pmc`` child runs of this script in ``--traffic-probe`` mode
+(FETCH_SIZE, then WRITE_SIZE, summed over the call's kernels), each scaled by
+what the same counter reads for a plain elementwise kernel of known size.
+``cpu_baseline`` is the fp32 CPU oracle (the reference's decode schedule) on a
+bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -50,6 +55,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--extra", action="store_true",
                     help="also time T=8/64 decode, T=4096 prefill and the attention layer")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC traffic runs")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--model", action="store_true",
                     help="also time the full 48-layer model (TTFT at 640 tokens, 256 greedy steps)")
     return ap.parse_args()
@@ -299,6 +306,81 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     }
 
 
+CAL_ELEMS = 64 << 20  # bf16 elements of the calibration kernel (128 MiB in, 128 MiB out)
+
+
+def traffic_probe(T):
+    """Child mode run under ``rocprofv3 --pmc``: decode-block calls over 8
+    rotating layers (9.7 GB of experts, beyond the 256 MB Infinity Cache),
+    then the calibration kernel: ``neg`` over CAL_ELEMS bf16 values (reads and
+    writes exactly 2 * CAL_ELEMS bytes)."""
+    import torch
+
+    from qmoe import _lib
+    from qmoe.moe import MoEBlock
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    layers = make_layers(8, dev, seed=3)
+    g = torch.Generator(device=dev).manual_seed(99)
+    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    res = torch.randn(T, H, generator=g, device=dev)
+    blocks = [MoEBlock(*w, K_TOP) for w in layers]
+    for _ in range(3):
+        for b in blocks:
+            b(x, res)
+    src = torch.randn(CAL_ELEMS, generator=g, device=dev).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def measure_traffic(T):
+    """HBM-side bytes per decode-block call from two rocprofv3 PMC runs of
+    ``--traffic-probe`` (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each
+    scaled by bytes / counter of the calibration kernel.  Returns a dict or
+    None (rocprofv3 missing or failed)."""
+    import csv
+    import shutil
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None
+    res = {}
+    with tempfile.TemporaryDirectory(prefix="qmoe_pmc_") as tmp:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            out = os.path.join(tmp, ctr)
+            cmd = [prof, "--pmc", ctr, "-d", out, "-o", "c", "--output-format", "csv", "--",
+                   sys.executable, os.path.abspath(__file__), "--traffic-probe", "--tokens", str(T)]
+            try:
+                subprocess.run(cmd, cwd=ROOT, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                               timeout=180, check=True)
+            except Exception as exc:  # noqa: BLE001 - reported, never fatal
+                print(f"[bench] traffic: {ctr} run failed: {exc}", file=sys.stderr, flush=True)
+                return None
+            files = [os.path.join(dp, f) for dp, _, fs in os.walk(out) for f in fs
+                     if f.endswith("counter_collection.csv")]
+            if not files:
+                return None
+            calls, cal = {}, []
+            for r in csv.DictReader(open(files[0])):
+                name, v = r["Kernel_Name"], float(r["Counter_Value"])
+                if "neg_kernel" in name and int(r["Grid_Size"]) * 8 >= CAL_ELEMS:
+                    cal.append(v)
+                elif "qmoe::block_" in name:
+                    calls.setdefault(name.split("(")[0], []).append(v)
+            if not cal or not calls:
+                return None
+            factor = 2.0 * CAL_ELEMS / (min(cal) * 1024.0)
+            # per call: the median dispatch of each kernel of the block, summed
+            per_call = sum(sorted(v)[len(v) // 2] for v in calls.values()) * 1024.0 * factor
+            res[ctr] = {"bytes_per_call": per_call, "scale": factor,
+                        "kernels": sorted(calls), "dispatches": sum(len(v) for v in calls.values())}
+    return res
+
+
 def cpu_baseline(layer, seconds, dev):
     """fp32 CPU oracle (reference decode schedule, qwen_with_nki.py:3456-3478)
     on one layer's weights: T=1 tokens with fresh random inputs until
@@ -342,6 +424,13 @@ def main():
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
               "(multi-GPU sharding is design-only)", file=sys.stderr)
         sys.exit(2)
+    if a.traffic_probe:
+        traffic_probe(a.tokens)
+        return
+    traffic = None
+    if not a.no_traffic and a.tokens <= 8:  # before this process touches the GPU
+        traffic = measure_traffic(a.tokens)
+        print(f"[bench] traffic: {traffic}", file=sys.stderr, flush=True)
     import torch
 
     from qmoe import _lib
@@ -404,15 +493,18 @@ def main():
         "moe_block_GBps": round(dec["block_GBps"], 1),
         "moe_block_hbm_frac": round(dec["block_frac"], 4),
         "roofline": {
-            "kernel": ("qmoe_moe_decode_block: block_router_kernel + block_gateup_kernel + "
-                       "block_down_combine_kernel (one call, 3 launches)") if a.tokens <= 8 else
+            "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
+                       "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else
                       "MoE block (route + moe_gateup_gemv_kernel + moe_down_gemv_kernel + combine)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": (round(traffic["FETCH_SIZE"]["bytes_per_call"] + traffic["WRITE_SIZE"]["bytes_per_call"])
+                        if traffic else None),
+            "traffic_detail": ({k: {"bytes": round(v["bytes_per_call"]), "scale": round(v["scale"], 4)}
+                                for k, v in traffic.items()} if traffic else None),
             "algorithmic_bytes_per_launch": dec["block_bytes"],
             "launch_us_mean": round(dec["us_per_block"], 3),
         },
