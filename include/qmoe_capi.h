@@ -203,7 +203,10 @@ int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, in
  *   x: bf16 [B*S, H]; wqkv: bf16 [(Hq+2*Hkv)*D, H] (q rows, then k, then v);
  *   q_norm_w, k_norm_w: bf16 [D]; rope_cos, rope_sin: f32 [max_pos, D/2];
  *   positions: i32 [B*S] (RoPE position == cache index of the token);
- *   q_out: bf16 [B*S, Hq, D]; k_cache, v_cache: bf16 [B, Hkv, S_max, D].
+ *   q_out: bf16 [B*S, Hq, D]; k_cache, v_cache: bf16 [B, Hkv, S_max, D];
+ *   workspace: f32, qmoe_qkv_norm_rope_workspace(B*S, H, Hq, Hkv, D) bytes
+ *   (decode-size token counts run the projection as an all-CU GEMV into it;
+ *   NULL allowed when that size is 0).
  *   Limits: D == 128, H % 64 == 0, positions < S_max and < max_pos.
  * Replaces: NeuronQwen3MoEAttention (qwen_with_nki.py:10081-10109): QKV
  *   projection, q_layernorm/k_layernorm (10102-10103) before RoPE
@@ -212,8 +215,15 @@ int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv, const qmoe_bf1
                        const qmoe_bf16* k_norm_w, const float* rope_cos, const float* rope_sin,
                        int64_t max_pos, const int32_t* positions, int64_t B, int64_t S,
                        int64_t H, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
-                       qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache,
+                       qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache, float* workspace,
                        qmoe_stream_t stream);
+
+/* Workspace bytes of qmoe_qkv_norm_rope for T = B*S token rows: T * (Hq +
+ * 2*Hkv) * D * 4 when T <= 16 and H in {512, 1024, 2048, 4096} with T*H <=
+ * 32768 (the GEMV path), else 0; -1 for negative sizes.
+ * Replaces: nothing in the reference (its kernels allocate their own HBM
+ *   scratch); the caller owns memory here. */
+int64_t qmoe_qkv_norm_rope_workspace(int64_t T, int64_t H, int64_t Hq, int64_t Hkv, int64_t D);
 
 /* Causal GQA flash attention for a prefill chunk.  Query s of batch b sits at
  * cache index start + s and sees cache entries [0, start + s].
@@ -225,8 +235,9 @@ int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_b
                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                       int64_t start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
 
-/* Decode attention (split-KV flash decoding), one query per batch row that
- * sees cache entries [0, ctx_len[b]).
+/* Decode attention (split-KV flash decoding on MFMA: one partial per 64
+ * cache entries, then a merge), one query per batch row that sees cache
+ * entries [0, ctx_len[b]).
  *   q: bf16 [B, Hq, D]; ctx_len: i32 [B] (1 <= ctx_len <= S_max);
  *   partial: f32 workspace of qmoe_attn_decode_workspace(B, Hq, D, S_max) floats;
  *   out: bf16 [B, Hq*D].  Limits: D == 128, Hq / Hkv <= 16.

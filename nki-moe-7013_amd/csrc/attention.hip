@@ -12,10 +12,14 @@
 //                    in the B-operand layout of O^T = V^T . P^T (the key order
 //                    inside each 16-key MFMA step is permuted to match; V is
 //                    stored transposed in LDS in that order).
-//  attn_decode    -- split-KV flash decoding: a workgroup owns one (batch, kv
-//                    head, 256-key split) and all q heads of that GQA group,
-//                    so each K/V row is read from HBM once; a second kernel
-//                    merges the splits.
+//  attn_decode    -- split-KV flash decoding on MFMA: a wave owns 64 keys of
+//                    one (batch, kv head) and all q heads of that GQA group
+//                    (S^T = K.Q^T, softmax per column, O^T = V^T.P^T), so each
+//                    K/V row is read from HBM once, with every load of the
+//                    wave in flight together; a second kernel merges the
+//                    per-wave partials that hold keys.
+#include "decode_util.hpp"
+#include "gemm.hpp"
 #include "mfma_tile.hpp"
 
 namespace qmoe {
@@ -23,52 +27,26 @@ namespace qmoe {
 constexpr int HD = 128;  // head_dim
 
 // ====================================================================== QKV
-__global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wqkv,
-    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-    const int32_t* __restrict__ positions, int T, int S, int H, int Hq, int Hkv, int S_max,
-    int max_pos, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[tile::SMEM_BYTES / 2];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int head = blockIdx.x;  // 0..Hq+2Hkv-1
-  const int m0 = blockIdx.y * tile::BM;
-  const int n0 = head * HD;
-  const int kc = (t & 7) * 8;
-  const uint16_t* ap[4];
-  const uint16_t* bp[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = tile::stage_row(t, j);
-    ap[j] = (m0 + r < T) ? x + int64_t(m0 + r) * H + kc : nullptr;
-    bp[j] = wqkv + int64_t(n0 + r) * H + kc;
-  }
-  tile::Acc acc;
-  tile::mma_128x128(ap, bp, H, smem, acc);  // ends with a barrier
-
-  constexpr int LDC = HD + 4;
-  float* ct = reinterpret_cast<float*>(smem);  // [128][LDC] fp32 (66 KB)
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-      const int col = tile::acc_col(wave, lane, ni);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ct[tile::acc_row(wave, lane, mi, i) * LDC + col] = acc.c[mi][ni][i];
-    }
-  __syncthreads();
-
-  const int row = t >> 1, half = t & 1;
-  const int tok = m0 + row;
-  // thread owns elements [32h, 32h+32) and their RoPE partners +64
+// Per-(token, head) finish shared by both QKV kernels: two threads (half = 0,
+// 1; lanes l and l^1) load the head's fp32 values v (LDS or global, 16-byte
+// aligned; elements [32h, 32h+32) and their RoPE partners +64) into
+// registers: q/k heads get the RMSNorm over head_dim and RoPE, then q goes to
+// q_out and k / v to the cache row at the token's position (rejected
+// positions write nothing).
+__device__ __forceinline__ void qkv_finish_head(
+    const float* v, int half, int tok, int head, const int32_t* __restrict__ positions, int S,
+    int Hq, int Hkv, int S_max, int max_pos, float eps, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cos,
+    const float* __restrict__ rope_sin, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
   float lo[32], hi[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    lo[i] = ct[row * LDC + half * 32 + i];
-    hi[i] = ct[row * LDC + 64 + half * 32 + i];
+  for (int i = 0; i < 32; i += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(v + half * 32 + i);
+    const float4 c = *reinterpret_cast<const float4*>(v + 64 + half * 32 + i);
+    lo[i] = a.x; lo[i + 1] = a.y; lo[i + 2] = a.z; lo[i + 3] = a.w;
+    hi[i] = c.x; hi[i + 1] = c.y; hi[i + 2] = c.z; hi[i + 3] = c.w;
   }
-  if (tok >= T) return;
   const int pos = positions[tok];
   if (pos < 0 || pos >= S_max || pos >= max_pos) return;  // rejected: nothing written
   const int b = tok / S;
@@ -111,6 +89,68 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
     *reinterpret_cast<u32x4*>(dst + half * 32 + c * 8) = v0;
     *reinterpret_cast<u32x4*>(dst + 64 + half * 32 + c * 8) = v1;
   }
+}
+
+// Decode-size QKV (T <= QKV_DEC_MAX_T token rows): the projection runs as a
+// bandwidth-bound GEMV over every CU (qmoe_gemm's register GEMV: all weight
+// rows streamed once) into an fp32 workspace [T][(Hq+2Hkv)*D]; this kernel
+// then finishes each (token, head) from there.
+constexpr int QKV_DEC_MAX_T = 16;
+
+__global__ __launch_bounds__(64) void qkv_finish_kernel(
+    const float* __restrict__ raw, const uint16_t* __restrict__ qn_w,
+    const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cos,
+    const float* __restrict__ rope_sin, const int32_t* __restrict__ positions, int T, int S, int Hq,
+    int Hkv, int S_max, int max_pos, float eps, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
+  const int t = threadIdx.x, head = blockIdx.x;
+  if (t >= 2 * T) return;
+  const int tok = t >> 1;
+  qkv_finish_head(raw + int64_t(tok) * (Hq + 2 * Hkv) * HD + head * HD, t & 1, tok, head, positions, S,
+                  Hq, Hkv, S_max, max_pos, eps, qn_w, kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
+}
+
+__global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wqkv,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+    const int32_t* __restrict__ positions, int T, int S, int H, int Hq, int Hkv, int S_max,
+    int max_pos, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[tile::SMEM_BYTES / 2];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int head = blockIdx.x;  // 0..Hq+2Hkv-1
+  const int m0 = blockIdx.y * tile::BM;
+  const int n0 = head * HD;
+  const int kc = (t & 7) * 8;
+  const uint16_t* ap[4];
+  const uint16_t* bp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = tile::stage_row(t, j);
+    ap[j] = (m0 + r < T) ? x + int64_t(m0 + r) * H + kc : nullptr;
+    bp[j] = wqkv + int64_t(n0 + r) * H + kc;
+  }
+  tile::Acc acc;
+  tile::mma_128x128(ap, bp, H, smem, acc);  // ends with a barrier
+
+  constexpr int LDC = HD + 4;
+  float* ct = reinterpret_cast<float*>(smem);  // [128][LDC] fp32 (66 KB)
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int col = tile::acc_col(wave, lane, ni);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ct[tile::acc_row(wave, lane, mi, i) * LDC + col] = acc.c[mi][ni][i];
+    }
+  __syncthreads();
+
+  const int row = t >> 1, half = t & 1;
+  const int tok = m0 + row;
+  if (tok >= T) return;
+  qkv_finish_head(ct + row * LDC, half, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
+                  kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
 }
 
 // ====================================================================== prefill
@@ -257,140 +297,229 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ====================================================================== decode
-constexpr int AD_SPLIT = 256;  // keys per workgroup
-constexpr int AD_MAX_G = 16;   // q heads per kv head
+constexpr int AD_SPLIT = 256;           // keys per workgroup
+constexpr int AD_WKEYS = 64;            // keys per wave; one partial (m, l, o) per wave
+constexpr int AD_SUBS = AD_SPLIT / AD_WKEYS;
+constexpr int AD_MAX_G = 16;            // q heads per kv head
+constexpr int AD_VT_LD = AD_WKEYS + 8;  // V^T row stride in LDS (bf16): 144 B, 16-byte aligned rows
+constexpr int AD_VCH = AD_WKEYS * HD / 8 / 64;  // 16-byte V chunks per lane (16)
+constexpr int AD_PSTR = HD + 4;         // partial record: m, l, 2 pad, o[HD] (16-byte aligned o)
 
+// Completes this wave's LDS writes before its own lanes read them (a wave's
+// DS instructions run in order; this also keeps the compiler from moving
+// reads above the writes).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Workgroup = (256-key split, kv head, batch row); each of its four waves
+// owns 64 keys and all G q heads of the group and writes its own partial
+// (m, l, o), so no wave waits on another.  Per wave, on v_mfma_f32_32x32x16_bf16:
+//   S^T [64 keys x 32] = K [64 x 128] . Q^T [128 x 32]   (q heads in columns
+//       0..G-1; K rows loaded from the cache straight into A-operand registers)
+//   softmax over keys per column: lane l holds column l % 32, 32 keys; one
+//       exchange with lane l ^ 32
+//   O^T [128 x 32] = V^T [128 x 64] . P^T [64 x 32]   (V^T and bf16 P^T through
+//       this wave's LDS)
+// Every global load of the wave is issued first (K, V, q), so a split costs
+// one HBM round trip.
 __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len, int Hq, int Hkv,
-    int S_max, int nsplit, float scale, float* __restrict__ partial) {
-  __shared__ float qs[AD_MAX_G][HD];
-  __shared__ float ps[AD_MAX_G][AD_SPLIT];
-  __shared__ float red[AD_MAX_G][4];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    int S_max, int nsub, float scale, float* __restrict__ partial) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt[AD_SUBS][HD][AD_VT_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[AD_SUBS][AD_MAX_G][AD_WKEYS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kvh = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
   const int ctx = min(ctx_len[b], S_max);
-  const int k0 = split * AD_SPLIT;
-  const int nk = min(AD_SPLIT, ctx - k0);
-  float* pout = partial + ((int64_t(b) * Hq + kvh * G) * nsplit + split) * (HD + 2);
-  // partial layout per (b, q head, split): [m, l, o[0..127]]
+  const int sub = blockIdx.x * AD_SUBS + wave;
+  const int kw0 = sub * AD_WKEYS;
+  const int nk = min(AD_WKEYS, ctx - kw0);
+  const int col = lane & 31, hi = lane >> 5;
+  // partial record per (b, q head, sub): [m, l, -, -, o[0..127]]
+  float* pbase = partial + (int64_t(b) * Hq + kvh * G) * nsub * AD_PSTR + int64_t(sub) * AD_PSTR;
+  const int64_t pstride = int64_t(nsub) * AD_PSTR;  // next q head
   if (nk <= 0) {
-    for (int i = t; i < G * (HD + 2); i += 256) {
-      const int g = i / (HD + 2), r = i - g * (HD + 2);
-      pout[int64_t(g) * nsplit * (HD + 2) + r] = (r == 0) ? -INFINITY : 0.0f;
+    if (lane < G) {
+      pbase[lane * pstride] = -INFINITY;
+      pbase[lane * pstride + 1] = 0.0f;
     }
     return;
   }
-  for (int i = t; i < G * HD; i += 256) {
-    const int g = i / HD, d = i - g * HD;
-    qs[g][d] = bf16_to_f32(q[(int64_t(b) * Hq + kvh * G + g) * HD + d]);
-  }
-  __syncthreads();
   const int64_t kv_base = (int64_t(b) * Hkv + kvh) * S_max * HD;
-  // scores: thread t owns key k0 + t
-  float sc[AD_MAX_G];
+  // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
+  u32x4 ka[2][HD / 16];
 #pragma unroll
-  for (int g = 0; g < AD_MAX_G; ++g) sc[g] = 0.0f;
-  if (t < nk) {
-    const uint16_t* kp = k_cache + kv_base + int64_t(k0 + t) * HD;
+  for (int mb = 0; mb < 2; ++mb) {
+    const uint16_t* kp = k_cache + kv_base + int64_t(kw0 + min(mb * 32 + col, nk - 1)) * HD + hi * 8;
 #pragma unroll
-    for (int c = 0; c < HD / 8; ++c) {
-      const u32x4 kv = ld16(kp + c * 8);
-      const float k8[8] = {bf16_lo(kv.x), bf16_hi(kv.x), bf16_lo(kv.y), bf16_hi(kv.y),
-                           bf16_lo(kv.z), bf16_hi(kv.z), bf16_lo(kv.w), bf16_hi(kv.w)};
+    for (int ks = 0; ks < HD / 16; ++ks) ka[mb][ks] = ld16(kp + ks * 16);
+  }
+  // V: lane l owns key pair (2*(l%32), 2*(l%32)+1) and dim chunks c = l/32 + 2i
+  // (8 dims each), both rows, so the transpose into LDS below writes whole
+  // 32-bit key pairs with lanes on consecutive banks
+  u32x4 vr[2][AD_VCH / 2];
 #pragma unroll
-      for (int g = 0; g < AD_MAX_G; ++g) {
-        if (g < G) {
+  for (int r = 0; r < 2; ++r) {
+    const uint16_t* vp = v_cache + kv_base + int64_t(kw0 + min(2 * col + r, nk - 1)) * HD + hi * 8;
 #pragma unroll
-          for (int u = 0; u < 8; ++u) sc[g] = fmaf(k8[u], qs[g][c * 8 + u], sc[g]);
-        }
+    for (int i = 0; i < AD_VCH / 2; ++i) vr[r][i] = ld16(vp + i * 16);
+  }
+  // Q^T as B operands: column col = q head, dims ks*16 + hi*8 (zero past G)
+  u32x4 qb[HD / 16];
+  const uint16_t* qp = q + (int64_t(b) * Hq + kvh * G + min(col, G - 1)) * HD + hi * 8;
+#pragma unroll
+  for (int ks = 0; ks < HD / 16; ++ks) qb[ks] = col < G ? ld16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+
+  // V^T into LDS: vt[wave][d][key], one 32-bit (key pair) write per dim
+#pragma unroll
+  for (int i = 0; i < AD_VCH / 2; ++i) {
+    const int d0 = (hi + 2 * i) * 8;
+    const uint32_t a4[4] = {vr[0][i].x, vr[0][i].y, vr[0][i].z, vr[0][i].w};
+    const uint32_t b4[4] = {vr[1][i].x, vr[1][i].y, vr[1][i].z, vr[1][i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<uint32_t*>(&vt[wave][d0 + 2 * j][2 * col]) = (a4[j] & 0xffffu) | (b4[j] << 16);
+      *reinterpret_cast<uint32_t*>(&vt[wave][d0 + 2 * j + 1][2 * col]) = (a4[j] >> 16) | (b4[j] & 0xffff0000u);
+    }
+  }
+
+  f32x16 sacc[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    sacc[mb] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks)
+      sacc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[mb][ks]),
+                                                         __builtin_bit_cast(bf16x8, qb[ks]), sacc[mb], 0,
+                                                         0, 0);
+  }
+  // element e of block mb: key mb*32 + (e/4)*8 + hi*4 + e%4, column col
+  float m = -INFINITY;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = mb * 32 + (e >> 2) * 8 + hi * 4 + (e & 3);
+      const float sv = key < nk ? sacc[mb][e] * scale : -INFINITY;
+      sacc[mb][e] = sv;
+      m = fmaxf(m, sv);
+    }
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  float l = 0.0f;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __expf(sacc[mb][e] - m);
+      sacc[mb][e] = p;
+      l += p;
+    }
+  l += __shfl_xor(l, 32, 64);
+  if (col < G) {  // P^T (bf16) into LDS: 4 consecutive keys per 8-byte write
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        u32x2 w;
+        w.x = pack_bf16x2(sacc[mb][e4 * 4 + 0], sacc[mb][e4 * 4 + 1]);
+        w.y = pack_bf16x2(sacc[mb][e4 * 4 + 2], sacc[mb][e4 * 4 + 3]);
+        *reinterpret_cast<u32x2*>(&pt[wave][col][mb * 32 + e4 * 8 + hi * 4]) = w;
       }
+  }
+  wave_lds_sync();
+
+  f32x16 oacc[HD / 32];
+#pragma unroll
+  for (int db = 0; db < HD / 32; ++db) oacc[db] = f32x16{};
+#pragma unroll
+  for (int ks = 0; ks < AD_WKEYS / 16; ++ks) {
+    const u32x4 pb = col < G ? *reinterpret_cast<const u32x4*>(&pt[wave][min(col, AD_MAX_G - 1)][ks * 16 + hi * 8])
+                             : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int db = 0; db < HD / 32; ++db) {
+      const u32x4 va = *reinterpret_cast<const u32x4*>(&vt[wave][db * 32 + col][ks * 16 + hi * 8]);
+      oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va),
+                                                         __builtin_bit_cast(bf16x8, pb), oacc[db], 0, 0, 0);
     }
   }
-  // max per head
-#pragma unroll
-  for (int g = 0; g < AD_MAX_G; ++g) {
-    if (g < G) {
-      const float s = (t < nk) ? sc[g] * scale : -INFINITY;
-      sc[g] = s;
-      const float m = wave_max(s);
-      if (lane == 0) red[g][wave] = m;
+  // element e of block db: d = db*32 + (e/4)*8 + hi*4 + e%4, column col = q head
+  if (col < G) {
+    float* pg = pbase + col * pstride;
+    if (hi == 0) {
+      pg[0] = m;
+      pg[1] = l;
     }
-  }
-  __syncthreads();
-  float mg[AD_MAX_G];
 #pragma unroll
-  for (int g = 0; g < AD_MAX_G; ++g)
-    mg[g] = (g < G) ? fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3])) : 0.0f;
-  __syncthreads();
+    for (int db = 0; db < HD / 32; ++db)
 #pragma unroll
-  for (int g = 0; g < AD_MAX_G; ++g) {
-    if (g < G) {
-      const float p = (t < nk) ? __expf(sc[g] - mg[g]) : 0.0f;
-      ps[g][t] = p;
-      const float l = wave_sum(p);
-      if (lane == 0) red[g][wave] = l;
-    }
-  }
-  __syncthreads();
-  // O[g][d] = sum_k p[g][k] V[k][d]; thread: d pair (t % 64) * 2, heads g = t/64 + 4*jg
-  const int d2 = (t & 63) * 2;
-  float oa[AD_MAX_G / 4][2];
-#pragma unroll
-  for (int jg = 0; jg < AD_MAX_G / 4; ++jg) oa[jg][0] = oa[jg][1] = 0.0f;
-  const uint16_t* vp = v_cache + kv_base + int64_t(k0) * HD + d2;
-  for (int kk = 0; kk < nk; ++kk) {
-    const uint32_t vv = *reinterpret_cast<const uint32_t*>(vp + int64_t(kk) * HD);
-    const float v0 = bf16_lo(vv), v1 = bf16_hi(vv);
-#pragma unroll
-    for (int jg = 0; jg < AD_MAX_G / 4; ++jg) {
-      const int g = wave + 4 * jg;
-      if (g < G) {
-        const float p = ps[g][kk];
-        oa[jg][0] = fmaf(p, v0, oa[jg][0]);
-        oa[jg][1] = fmaf(p, v1, oa[jg][1]);
-      }
-    }
-  }
-#pragma unroll
-  for (int jg = 0; jg < AD_MAX_G / 4; ++jg) {
-    const int g = wave + 4 * jg;
-    if (g < G) {
-      float* pg = pout + int64_t(g) * nsplit * (HD + 2);
-      if ((t & 63) == 0) {
-        pg[0] = mg[g];
-        pg[1] = red[g][0] + red[g][1] + red[g][2] + red[g][3];
-      }
-      pg[2 + d2] = oa[jg][0];
-      pg[2 + d2 + 1] = oa[jg][1];
-    }
+      for (int e4 = 0; e4 < 4; ++e4)
+        *reinterpret_cast<float4*>(pg + 4 + db * 32 + e4 * 8 + hi * 4) =
+            make_float4(oacc[db][e4 * 4], oacc[db][e4 * 4 + 1], oacc[db][e4 * 4 + 2], oacc[db][e4 * 4 + 3]);
   }
 }
 
+// Merge of the partials that hold keys (ceil(ctx / AD_WKEYS) of them), in
+// chunks of HD partials: thread i reads partial i's (m, l) and its weight
+// exp(m - M) goes to LDS; then every thread (one output dim d) adds its o[d]
+// of the chunk, eight loads in flight at a time.
 __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __restrict__ partial,
-                                                               int nsplit,
+                                                               const int32_t* __restrict__ ctx_len,
+                                                               int Hq, int S_max, int nsub,
                                                                uint16_t* __restrict__ out) {
+  __shared__ float sw[HD];
+  __shared__ float sred[2];
   const int bh = blockIdx.x;  // b * Hq + h
-  const int d = threadIdx.x;
-  const float* p = partial + int64_t(bh) * nsplit * (HD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p[int64_t(s) * (HD + 2)]);
+  const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
+  const int ctx = min(ctx_len[bh / Hq], S_max);
+  const int live = min(nsub, (ctx + AD_WKEYS - 1) / AD_WKEYS);
+  const float* p = partial + int64_t(bh) * nsub * AD_PSTR;
+  float mloc = -INFINITY;
+  for (int s = d; s < live; s += HD) mloc = fmaxf(mloc, p[int64_t(s) * AD_PSTR]);
+  mloc = wave_max(mloc);
+  if (lane == 0) sred[wave] = mloc;
+  __syncthreads();
+  const float M = fmaxf(sred[0], sred[1]);
   float L = 0.0f, O = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* ps = p + int64_t(s) * (HD + 2);
-    const float m = ps[0];
-    if (m == -INFINITY) continue;
-    const float w = __expf(m - M);
-    L += ps[1] * w;
-    O += ps[2 + d] * w;
+  for (int c0 = 0; c0 < live; c0 += HD) {
+    const int n = min(HD, live - c0);
+    __syncthreads();
+    if (d < n) {
+      const float m = p[int64_t(c0 + d) * AD_PSTR];
+      sw[d] = m == -INFINITY ? 0.0f : __expf(m - M);
+      L += sw[d] * p[int64_t(c0 + d) * AD_PSTR + 1];  // summed over threads below
+    }
+    __syncthreads();
+    for (int s0 = 0; s0 < n; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = s0 + u < n ? p[int64_t(c0 + s0 + u) * AD_PSTR + 4 + d] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < n) O = fmaf(sw[s0 + u], v[u], O);
+    }
   }
-  out[int64_t(bh) * HD + d] = f32_to_bf16(O / L);
+  L = wave_sum(L);
+  __syncthreads();
+  if (lane == 0) sred[wave] = L;
+  __syncthreads();
+  out[int64_t(bh) * HD + d] = f32_to_bf16(O / (sred[0] + sred[1]));
 }
 
 }  // namespace qmoe
 
 using namespace qmoe;
+
+// The GEMV + finish path: decode-size token counts whose activations fit the
+// register GEMV (K = H in {512, 1024, 2048, 4096}, T * H <= 32768).
+static bool qkv_decode_path(int64_t T, int64_t H) {
+  return T <= QKV_DEC_MAX_T && (H == 512 || H == 1024 || H == 2048 || H == 4096) && T * H <= 32768;
+}
+
+extern "C" int64_t qmoe_qkv_norm_rope_workspace(int64_t T, int64_t H, int64_t Hq, int64_t Hkv,
+                                                int64_t D) {
+  if (T < 0 || H < 0 || Hq < 0 || Hkv < 0 || D < 0) return -1;
+  return qkv_decode_path(T, H) ? T * (Hq + 2 * Hkv) * D * int64_t(sizeof(float)) : 0;
+}
 
 extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                                   const qmoe_bf16* q_norm_w, const qmoe_bf16* k_norm_w,
@@ -398,7 +527,7 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                                   const int32_t* positions, int64_t B, int64_t S, int64_t H,
                                   int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
                                   qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache,
-                                  qmoe_stream_t stream) {
+                                  float* workspace, qmoe_stream_t stream) {
   QMOE_REQUIRE(x && wqkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && q_out &&
                    k_cache && v_cache,
                "qmoe_qkv_norm_rope: null pointer");
@@ -410,11 +539,21 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
   QMOE_REQUIRE(S_max > 0 && max_pos > 0, "qmoe_qkv_norm_rope: bad S_max/max_pos");
   const int64_t T = B * S;
   if (T == 0) return QMOE_OK;
+  const int max_p = int(std::min<int64_t>(max_pos, 1ll << 30));
+  if (qkv_decode_path(T, H)) {
+    QMOE_REQUIRE(workspace, "qmoe_qkv_norm_rope: T <= 16 needs the workspace");
+    const int64_t N = (Hq + 2 * Hkv) * HD;
+    int rc = gemm_launch(x, H, wqkv, T, N, H, QMOE_GEMM_STORE_F32, workspace, N, as_stream(stream));
+    if (rc) return rc;
+    hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv)), dim3(64), 0, as_stream(stream),
+                       workspace, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(T), int(S),
+                       int(Hq), int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
+    return hip_status("qmoe_qkv_norm_rope(finish)");
+  }
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + tile::BM - 1) / tile::BM));
   hipLaunchKernelGGL(qkv_norm_rope_kernel, grid, dim3(256), 0, as_stream(stream), x, wqkv, q_norm_w,
                      k_norm_w, rope_cos, rope_sin, positions, int(T), int(S), int(H), int(Hq),
-                     int(Hkv), int(S_max), int(std::min<int64_t>(max_pos, 1ll << 30)), eps, q_out,
-                     k_cache, v_cache);
+                     int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
   return hip_status("qmoe_qkv_norm_rope");
 }
 
@@ -436,8 +575,8 @@ extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
 }
 
 extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t S_max) {
-  const int64_t nsplit = (S_max + AD_SPLIT - 1) / AD_SPLIT;
-  return B * Hq * nsplit * (D + 2);
+  const int64_t nsub = (S_max + AD_SPLIT - 1) / AD_SPLIT * AD_SUBS;
+  return B * Hq * nsub * (D + 4);
 }
 
 extern "C" int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache,
@@ -451,13 +590,14 @@ extern "C" int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   QMOE_REQUIRE(B >= 0 && B < 65536 && S_max > 0, "qmoe_attn_decode: bad B/S_max");
   if (B == 0) return QMOE_OK;
   const int nsplit = int((S_max + AD_SPLIT - 1) / AD_SPLIT);
+  const int nsub = nsplit * AD_SUBS;
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(attn_decode_split_kernel, dim3(unsigned(nsplit), unsigned(Hkv), unsigned(B)),
-                     dim3(256), 0, s, q, k_cache, v_cache, ctx_len, int(Hq), int(Hkv), int(S_max),
-                     nsplit, scale, partial);
+                     dim3(256), 0, s, q, k_cache, v_cache, ctx_len, int(Hq), int(Hkv), int(S_max), nsub,
+                     scale, partial);
   int rc = hip_status("qmoe_attn_decode(split)");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(unsigned(B * Hq)), dim3(HD), 0, s, partial, nsplit,
-                     out);
+  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(unsigned(B * Hq)), dim3(HD), 0, s, partial, ctx_len,
+                     int(Hq), int(S_max), nsub, out);
   return hip_status("qmoe_attn_decode(merge)");
 }

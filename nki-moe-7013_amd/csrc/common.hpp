@@ -67,6 +67,21 @@ __device__ __forceinline__ float dot8(const u32x4& w, const float* x) {
   return s;
 }
 
+// acc + dot of 8 bf16 pairs, both operands packed (u32x4 = 8 bf16): four
+// v_dot2c_f32_bf16 (each adds lo*lo + hi*hi to the fp32 accumulator; the
+// bf16 products are exact in fp32).  No unpacking of either operand.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b),
+                                         acc, false);
+}
+__device__ __forceinline__ float dot8_bf16(const u32x4& a, const u32x4& b, float acc) {
+  acc = dot2_bf16(a.x, b.x, acc);
+  acc = dot2_bf16(a.y, b.y, acc);
+  acc = dot2_bf16(a.z, b.z, acc);
+  return dot2_bf16(a.w, b.w, acc);
+}
+
 // ---------------------------------------------------------------- reductions (wave64)
 // DPP-based: row_shr 1/2/4/8 leave each 16-lane row's total in its lane 15,
 // row_bcast:15 / row_bcast:31 fold the rows so lane 63 holds the wave total,

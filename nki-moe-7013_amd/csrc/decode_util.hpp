@@ -19,6 +19,26 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
 }
 
+// Copies n 16-byte chunks into LDS (dst[c] = *src(c)) with NT threads.  Up to
+// MAXI chunks per thread are all loaded before the first is stored, so the
+// copy costs one memory round trip (a plain strided loop would wait for each
+// load before issuing the next); chunks beyond NT * MAXI take a loop.
+template <int NT, int MAXI, class Src>
+__device__ __forceinline__ void stage16(u32x4* dst, int n, Src src) {
+  u32x4 v[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    const int c = int(threadIdx.x) + NT * i;
+    if (c < n) v[i] = ld16(src(c));
+  }
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    const int c = int(threadIdx.x) + NT * i;
+    if (c < n) dst[c] = v[i];
+  }
+  for (int c = int(threadIdx.x) + NT * MAXI; c < n; c += NT) dst[c] = ld16(src(c));
+}
+
 // Stage n token rows (bf16 [H]) into LDS; rows given by an index map or direct.
 __device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* src,
                                                 const int32_t* row_map, int r0, int n, int H) {

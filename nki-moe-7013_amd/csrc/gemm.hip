@@ -6,6 +6,7 @@
 //    non-temporal loads (K/512 loads per row per lane, all in flight), and
 //    reduces the per-lane partial dots with cross-lane shuffles.
 //  * M > 16: the direct-to-LDS MFMA pipeline (mfma_pipe.hpp).
+#include "decode_util.hpp"
 #include "gemm.hpp"
 #include "mfma_pipe.hpp"
 
@@ -31,10 +32,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   // stage the M activation rows (16-byte chunks)
   const int kchunks = K / 8;
-  for (int c = t; c < M * kchunks; c += 256) {
-    const int m = c / kchunks, kc = c - m * kchunks;
-    *reinterpret_cast<u32x4*>(xs + m * K + kc * 8) = ld16(A + m * lda + kc * 8);
-  }
+  stage16<256, 16>(reinterpret_cast<u32x4*>(xs), M * kchunks, [&](int c) {
+    const int m = c / kchunks;
+    return A + m * lda + (c - m * kchunks) * 8;
+  });
   __syncthreads();
 
   const int n0 = (blockIdx.x * 4 + wave) * R;
@@ -73,6 +74,108 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
         if (lane == 0 && n0 + r < N) store_out<MODE>(C, int64_t(m) * ldc + n0 + r, v);
       }
     }
+  }
+}
+
+// GEMV for K = 512 * KC <= 4096: every weight load of a wave (R rows x KC
+// 16-byte chunks per lane) is issued before the activation rows are staged,
+// so the weight stream starts with the workgroup and all of it is in flight
+// at once (R * KC <= 16 loads per lane).
+template <int MT, int R, int KC, int MODE>
+__global__ __launch_bounds__(256) void gemv_reg_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                       const uint16_t* __restrict__ B, int M, int N,
+                                                       int K, void* __restrict__ C, int64_t ldc) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * R;
+  u32x4 w[R][KC];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint16_t* brow = B + int64_t(min(n0 + r, N - 1)) * K + lane * 8;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) w[r][c] = ld_stream(brow + c * 512);
+  }
+  const int kchunks = K / 8;
+  stage16<256, 16>(reinterpret_cast<u32x4*>(xs), M * kchunks, [&](int c) {
+    const int m = c / kchunks;
+    return A + m * lda + (c - m * kchunks) * 8;
+  });
+  __syncthreads();
+  float acc[MT][R];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < M) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + m * K + c * 512 + lane * 8);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = dot8_bf16(w[r][c], xv, acc[m][r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m < M) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float v = wave_sum(acc[m][r]);
+        if (lane == 0 && n0 + r < N) store_out<MODE>(C, int64_t(m) * ldc + n0 + r, v);
+      }
+    }
+  }
+}
+
+// Skinny GEMM for 2 <= M <= 16 rows of A (batched decode), K = 128 * KS:
+// v_mfma_f32_16x16x32_bf16 with the A rows padded to 16 (zeros past M).  A
+// workgroup owns NB (8 or 16) output columns; wave w owns the K range
+// [w*K/4, (w+1)*K/4): its KS B operands (16 bytes of a weight row each, lane
+// l -> column l % 16, k offset (l / 16) * 8) are all loaded before A is
+// staged, the KS MFMAs accumulate, and the four waves' 16x16 partials are
+// added in wave order through LDS.  HBM-bound like the M = 1 GEMV: the
+// arithmetic that makes dot-product GEMVs slow at M = 8 costs KS MFMAs here.
+template <int NB, int KS, int MODE>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                        const uint16_t* __restrict__ B, int M, int N,
+                                                        int K, void* __restrict__ C, int64_t ldc) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [M][K] bf16
+  __shared__ float red[4][16][17];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int n0 = blockIdx.x * NB;
+  const int col = lane & 15, kq = lane >> 4;
+  const int kw = wave * (K / 4);
+  u32x4 bw[KS];
+  {
+    const bool live = col < NB && n0 + col < N;
+    const uint16_t* bp = B + int64_t(min(n0 + col, N - 1)) * K + kw + kq * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bw[s] = live ? ld_stream(bp + s * 32) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const int kchunks = K / 8;
+  stage16<256, 16>(reinterpret_cast<u32x4*>(xs), M * kchunks, [&](int c) {
+    const int m = c / kchunks;
+    return A + m * lda + (c - m * kchunks) * 8;
+  });
+  __syncthreads();
+  f32x4 acc = f32x4{};
+  const uint16_t* ap = xs + min(col, M - 1) * K + kw + kq * 8;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const u32x4 a = col < M ? *reinterpret_cast<const u32x4*>(ap + s * 32) : u32x4{0u, 0u, 0u, 0u};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, bw[s]), acc, 0, 0, 0);
+  }
+  // lane l holds column l % 16, rows (l / 16) * 4 + 0..3
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][kq * 4 + i][col] = acc[i];
+  __syncthreads();
+  const int m = t >> 4, n = t & 15;
+  if (m < M && n < NB && n0 + n < N) {
+    const float v = ((red[0][m][n] + red[1][m][n]) + red[2][m][n]) + red[3][m][n];
+    store_out<MODE>(C, int64_t(m) * ldc + n0 + n, v);
   }
 }
 
@@ -140,25 +243,107 @@ static int launch_pipe(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
 
 // Tile shape by how many tiles the problem has: 256x256 (one workgroup per
 // CU, least L2 traffic per flop) once it fills the GPU, else smaller tiles
-// with two workgroups per CU.
+// with two workgroups per CU; problems that would still leave most CUs idle
+// (the prefill router: 4096 x 128 x 2048) take 64x64 tiles with four stages
+// in flight, since each of their few workgroups walks a long K.
 template <int MODE>
 static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                        void* C, int64_t ldc, hipStream_t s) {
   using Big = pipe::Pipe<256, 256, 64, 2>;
   using Mid = pipe::Pipe<128, 256, 32, 3>;
   using Small = pipe::Pipe<128, 128, 64, 2>;
+  using Tiny = pipe::Pipe<64, 64, 64, 4>;
   auto count = [&](int bm, int bn) { return int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (count(256, 256) >= 224) return launch_pipe<Big, 1, MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (count(128, 256) >= 224) return launch_pipe<Mid, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
-  return launch_pipe<Small, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
+  if (count(128, 128) >= 96) return launch_pipe<Small, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
+  return launch_pipe<Tiny, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
 }
 
 // ------------------------------------------------------------------ launcher
+template <int MT, int MODE>
+static int launch_gemv_reg(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                           void* C, int64_t ldc, hipStream_t s) {
+  const size_t shm = size_t(M) * K * 2;
+  static const bool attr = [] {
+    for (const void* f : {reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 1, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 2, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 4, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 2, 8, MODE>)})
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+    return true;
+  }();
+  (void)attr;
+  switch (K / 512) {
+#define QMOE_GR(R, KC)                                                                            \
+  case KC:                                                                                        \
+    hipLaunchKernelGGL((gemv_reg_kernel<MT, R, KC, MODE>), dim3(unsigned((N + 4 * R - 1) / (4 * R))), \
+                       dim3(256), shm, s, A, lda, B, M, N, K, C, ldc);                            \
+    return hip_status("qmoe_gemm(gemv)");
+    QMOE_GR(4, 1)
+    QMOE_GR(4, 2)
+    QMOE_GR(4, 4)
+    QMOE_GR(2, 8)
+#undef QMOE_GR
+    default:
+      return fail(QMOE_ERR_INVALID, "qmoe_gemm: gemv register path needs K in {512, 1024, 2048, 4096}");
+  }
+}
+
+template <int MODE>
+static int launch_gemv_mfma(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                            void* C, int64_t ldc, hipStream_t s) {
+  const size_t shm = size_t(M) * K * 2;
+  const bool narrow = (N + 15) / 16 < 256;  // 8 columns per workgroup to fill the CUs
+  static const bool attr = [] {
+    for (const void* f : {reinterpret_cast<const void*>(gemv_mfma_kernel<8, 4, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<16, 4, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<8, 8, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<16, 8, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<8, 16, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<16, 16, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<8, 32, MODE>),
+                          reinterpret_cast<const void*>(gemv_mfma_kernel<16, 32, MODE>)})
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+    return true;
+  }();
+  (void)attr;
+  switch (K / 128) {
+#define QMOE_GM(KS)                                                                                \
+  case KS:                                                                                         \
+    if (narrow)                                                                                    \
+      hipLaunchKernelGGL((gemv_mfma_kernel<8, KS, MODE>), dim3(unsigned((N + 7) / 8)), dim3(256), shm, \
+                         s, A, lda, B, M, N, K, C, ldc);                                           \
+    else                                                                                           \
+      hipLaunchKernelGGL((gemv_mfma_kernel<16, KS, MODE>), dim3(unsigned((N + 15) / 16)), dim3(256),  \
+                         shm, s, A, lda, B, M, N, K, C, ldc);                                      \
+    return hip_status("qmoe_gemm(gemv mfma)");
+    QMOE_GM(4)
+    QMOE_GM(8)
+    QMOE_GM(16)
+    QMOE_GM(32)
+#undef QMOE_GM
+    default:
+      return fail(QMOE_ERR_INVALID, "qmoe_gemm: skinny MFMA path needs K in {512, 1024, 2048, 4096}");
+  }
+}
+
 template <int MODE>
 static int launch_gemv(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                        void* C, int64_t ldc, hipStream_t s) {
   const size_t shm = size_t(M) * K * 2;
-  const bool wide = N >= 4096;
+  const int kc = K / 512;
+  if (M >= 2 && (kc == 1 || kc == 2 || kc == 4 || kc == 8))
+    return launch_gemv_mfma<MODE>(A, lda, B, M, N, K, C, ldc, s);
+  if (kc == 1 || kc == 2 || kc == 4 || kc == 8) {
+    if (M <= 1) return launch_gemv_reg<1, MODE>(A, lda, B, M, N, K, C, ldc, s);
+    if (M <= 4) return launch_gemv_reg<4, MODE>(A, lda, B, M, N, K, C, ldc, s);
+    if (M <= 8) return launch_gemv_reg<8, MODE>(A, lda, B, M, N, K, C, ldc, s);
+    return launch_gemv_reg<16, MODE>(A, lda, B, M, N, K, C, ldc, s);
+  }
+  // 16 rows per workgroup (4 per wave) for wide outputs, and whenever the
+  // staged activations are large (fewer workgroups re-staging them)
+  const bool wide = N >= 4096 || shm > 16384;
   const int rows_per_block = wide ? 16 : 4;
   dim3 grid((N + rows_per_block - 1) / rows_per_block);
 #define QMOE_GEMV(MT)                                                                        \

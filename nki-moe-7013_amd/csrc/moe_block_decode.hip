@@ -133,10 +133,21 @@ __global__ __launch_bounds__(256 * GR) void block_expert_kernel(
   const int tid = threadIdx.x, grp = tid >> 8, gt = tid & 255, lane = tid & 63, wave = gt >> 6;
   float* s_red = reinterpret_cast<float*>(s_x + T * H);
 
-  for (int q = tid; q < T * E; q += NT) s_log[q] = logits[q];
+  // logits and x rows: every load issued before the first LDS store
+  float lg[(BLK_MAX_T * ROUTER_MAX_E + NT - 1) / NT];
+#pragma unroll
+  for (int i = 0; i < (BLK_MAX_T * ROUTER_MAX_E + NT - 1) / NT; ++i) {
+    const int q = tid + NT * i;
+    lg[i] = q < T * E ? logits[q] : 0.0f;
+  }
+  stage16<NT, (BLK_MAX_T * 4096 / 8 + NT - 1) / NT>(reinterpret_cast<u32x4*>(s_x), T * H / 8,
+                                                    [&](int q) { return x + int64_t(q) * 8; });
+#pragma unroll
+  for (int i = 0; i < (BLK_MAX_T * ROUTER_MAX_E + NT - 1) / NT; ++i) {
+    const int q = tid + NT * i;
+    if (q < T * E) s_log[q] = lg[i];
+  }
   for (int q = tid; q < E; q += NT) s_tm[q] = 0u;
-  for (int q = tid; q < T * H / 8; q += NT)
-    reinterpret_cast<u32x4*>(s_x)[q] = ld16(x + int64_t(q) * 8);
   __syncthreads();
   for (int t = tid >> 6; t < T; t += NT / 64)
     topk_softmax_wave(s_log + t * E, E, k, s_idx + t * k, s_w + t * k);

@@ -43,8 +43,9 @@ PROTOTYPES = {
     "qmoe_gemm": (c_int, [P, I64, P, I64, I64, I64, c_int, P, I64, P]),
     "qmoe_qkv_norm_rope": (
         c_int,
-        [P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, I64, c_float, P, P, P, P],
+        [P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, I64, c_float, P, P, P, P, P],
     ),
+    "qmoe_qkv_norm_rope_workspace": (c_int64, [I64, I64, I64, I64, I64]),
     "qmoe_attn_prefill": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, I64, c_float, P, P]),
     "qmoe_attn_decode_workspace": (c_int64, [I64, I64, I64, I64]),
     "qmoe_attn_decode": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, c_float, P, P, P]),

@@ -57,8 +57,13 @@ class Attention:
         S > 1: causal prefill of a chunk starting at cache index ``start``.
         S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1).
         """
+        qws = self._ws.get(("qkv", B * S))
+        if qws is None:
+            n = ops.qkv_norm_rope_workspace(B * S, x.shape[1], self.n_q, self.n_kv, self.head_dim)
+            qws = torch.empty(max(n // 4, 1), dtype=torch.float32, device=x.device)
+            self._ws[("qkv", B * S)] = qws
         q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
-                              self.n_q, self.n_kv, cache.k, cache.v, self.eps)
+                              self.n_q, self.n_kv, cache.k, cache.v, self.eps, workspace=qws)
         if S > 1:
             o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
         else:

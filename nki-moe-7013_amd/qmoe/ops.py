@@ -391,10 +391,11 @@ def qkv_norm_rope(
     x: torch.Tensor, wqkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
     rope_cos: torch.Tensor, rope_sin: torch.Tensor, positions: torch.Tensor,
     B: int, S: int, Hq: int, Hkv: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
-    eps: float, q_out: Optional[torch.Tensor] = None,
+    eps: float, q_out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """QKV projection + per-head RMSNorm + RoPE; K/V written into the cache.
-    Returns ``q[B*S, Hq, D]`` (bf16)."""
+    Returns ``q[B*S, Hq, D]`` (bf16).  ``workspace`` (f32, at least
+    :func:`qkv_norm_rope_workspace` bytes) is allocated here when not given."""
     T, H = x.shape
     D = q_norm_w.shape[0]
     if T != B * S:
@@ -414,16 +415,29 @@ def qkv_norm_rope(
     _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
     q_out = torch.empty(T, Hq, D, dtype=BF16, device=x.device) if q_out is None else q_out
     _need(q_out, "q_out", BF16, (T, Hq, D))
-    _same_device(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, k_cache, v_cache, q_out)
+    ws_bytes = qkv_norm_rope_workspace(T, H, Hq, Hkv, D)
+    if workspace is None and ws_bytes > 0:
+        workspace = torch.empty(ws_bytes // 4, dtype=F32, device=x.device)
+    if workspace is not None:
+        _need(workspace, "workspace", F32)
+        if workspace.numel() * 4 < ws_bytes:
+            raise ValueError(f"workspace: need {ws_bytes} bytes, got {workspace.numel() * 4}")
+    _same_device(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, k_cache, v_cache, q_out,
+                 workspace)
     check(
         lib().qmoe_qkv_norm_rope(
             _ptr(x), _ptr(wqkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cos), _ptr(rope_sin),
             max_pos, _ptr(positions), B, S, H, Hq, Hkv, D, S_max, float(eps), _ptr(q_out),
-            _ptr(k_cache), _ptr(v_cache), _stream(),
+            _ptr(k_cache), _ptr(v_cache), _ptr(workspace), _stream(),
         ),
         "qmoe_qkv_norm_rope",
     )
     return q_out
+
+
+def qkv_norm_rope_workspace(T: int, H: int, Hq: int, Hkv: int, D: int) -> int:
+    """Bytes of f32 workspace :func:`qkv_norm_rope` needs for ``T`` token rows."""
+    return int(lib().qmoe_qkv_norm_rope_workspace(T, H, Hq, Hkv, D))
 
 
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, B: int, S: int,

@@ -62,7 +62,9 @@ def test_version():
                                            1, 1, 1, 1, 1 << 30, None, 1, None), "exactly one"),
         (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 100, 128, 8,
                                            1, 1, 1, 1, 1 << 30, None, 1, None), "multiple of 32"),
-        (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 1, 1, 2048, 32, 4, 64, 10, 1e-6, 1, 1, 1, None), "head_dim"),
+        (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 1, 1, 2048, 32, 4, 64, 10, 1e-6, 1, 1, 1, 1, None), "head_dim"),
+        (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 8, 1, 2048, 32, 4, 128, 10, 1e-6, 1, 1, 1, None, None),
+         "needs the workspace"),
         (lambda l: l.qmoe_attn_prefill(1, 1, 1, 1, 10, 32, 4, 128, 8, 0, 0.1, 1, None), "S_max"),
         (lambda l: l.qmoe_attn_decode(1, 1, 1, 1, 1, 64, 2, 128, 16, 0.1, 1, 1, None), "Hq / Hkv <= 16"),
     ],

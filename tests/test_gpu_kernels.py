@@ -33,7 +33,9 @@ def _fp32_reference_matmuls():
 @pytest.mark.parametrize("M,N,K", [(1, 256, 2048), (5, 4096, 2048), (16, 128, 2048), (8, 2048, 4096),
                                    (128, 256, 2048), (300, 384, 768), (77, 2048, 4096),
                                    # ragged N; 128x256 tiles; 256x256 tiles
-                                   (300, 200, 128), (4096, 2048, 1024), (4096, 4096, 256)])
+                                   (300, 200, 128), (4096, 2048, 1024), (4096, 4096, 256),
+                                   # the prefill router shape (64x64 tiles, four stages)
+                                   (4096, 128, 2048)])
 def test_gemm_vs_fp32(dev, M, N, K):
     announce(f"gemm M={M} N={N} K={K}")
     g = torch.Generator(device=dev).manual_seed(M * 7 + N)
@@ -136,7 +138,10 @@ def _random_topk(T, k, E, seed, skew=None):
     return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
 
 
-@pytest.mark.parametrize("T,skew", [(1, None), (8, None), (64, None), (333, None), (4096, None), (4096, 1.1)])
+# T*k <= 4096 pairs: single-workgroup kernel; above: chunked rank + place kernels
+# (513: a ragged last chunk; 16384: 32 chunks, the most the place kernel holds).
+@pytest.mark.parametrize("T,skew", [(1, None), (8, None), (64, None), (333, None), (512, None), (513, 1.1),
+                                    (4096, None), (4096, 1.1), (16384, 1.1)])
 def test_permute_bit_exact(dev, T, skew):
     announce(f"permute T={T} skew={skew}")
     top = _random_topk(T, K_TOP, E, T, skew)
@@ -155,14 +160,17 @@ def test_permute_bit_exact(dev, T, skew):
     assert torch.equal(route.active.cpu()[:n_active], torch.from_numpy(ref["active"]))
 
 
-def test_permute_rejects_out_of_range_ids(dev):
-    announce("permute with an out-of-range expert id")
-    top = torch.tensor([[0, 1], [2, 200]], dtype=torch.int32, device=dev)
+@pytest.mark.parametrize("T", [2, 1000])
+def test_permute_rejects_out_of_range_ids(dev, T):
+    announce(f"permute with an out-of-range expert id T={T}")
+    top = torch.from_numpy(_random_topk(T, 8, 8, 5)).to(dev)
+    top[T // 2, 3] = 200  # one bad id (in the last chunk's neighbourhood for T = 1000)
     route = ops.moe_permute(top, 8, 128)
     torch.cuda.synchronize()
     meta = route.meta.cpu()
     assert int(meta[2]) == 1 and int(meta[0]) == 0 and int(meta[1]) == 0
-    assert sorted(route.token_slot.cpu().tolist()) == [0, 1, 2, 3]
+    assert torch.equal(route.token_slot.cpu(), torch.arange(T * 8, dtype=torch.int32))
+    assert torch.equal(route.slot_token.cpu(), torch.arange(T * 8, dtype=torch.int32) // 8)
 
 
 # --------------------------------------------------------------------------- experts
@@ -310,7 +318,9 @@ def _rope(max_pos, dev):
     return cos[:, : D // 2].contiguous().to(dev), sin[:, : D // 2].contiguous().to(dev)
 
 
-@pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0)])
+# B*S <= 16: GEMV + finish path (8, 16: batched decode steps); larger: MFMA tile path
+@pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0), (8, 1, 1279), (16, 1, 40),
+                                       (1, 1, 0)])
 def test_qkv_norm_rope(dev, attn_w, B, S, start):
     announce(f"qkv_norm_rope B={B} S={S} start={start}")
     wqkv, qn, kn = attn_w
