@@ -59,6 +59,8 @@ def parse():
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--model", action="store_true",
                     help="also time the full 48-layer model (TTFT at 640 tokens, 256 greedy steps)")
+    ap.add_argument("--only-model", action="store_true",
+                    help="time only the full model, in this process, and print its numbers as JSON")
     return ap.parse_args()
 
 
@@ -277,13 +279,18 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     cfg = qn.Qwen3MoeInferenceConfig(nc)
     cfg.num_hidden_layers = n_layers
     m = qn.NeuronQwen3MoeForCausalLM(None, cfg)
+    t0 = time.perf_counter()
     m.load()
+    torch.cuda.synchronize()
+    print(f"[bench] model: 48 layers loaded (random init) in {time.perf_counter() - t0:.1f}s",
+          file=sys.stderr, flush=True)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(0))
-    for _ in range(2):  # warm-up (lazy allocations, graph capture)
+    for w in range(2):  # warm-up (lazy allocations, graph capture)
         m.reset()
         first = m.prefill(prompt).argmax(-1)
         m.greedy_decode(first, 4)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        print(f"[bench] model: warm-up {w} done", file=sys.stderr, flush=True)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     m.reset()
     ev[0].record()
@@ -428,7 +435,7 @@ def main():
         traffic_probe(a.tokens)
         return
     traffic = None
-    if not a.no_traffic and a.tokens <= 8:  # before this process touches the GPU
+    if not a.no_traffic and not a.only_model and a.tokens <= 8:  # before this process touches the GPU
         traffic = measure_traffic(a.tokens)
         print(f"[bench] traffic: {traffic}", file=sys.stderr, flush=True)
     import torch
@@ -438,6 +445,12 @@ def main():
     _lib.lib()
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if a.only_model:
+        res = bench_model(dev)
+        print(f"[bench] model: {res}", file=sys.stderr, flush=True)
+        print(json.dumps({"workload": "Qwen3-30B-A3B-shaped model, 48 layers, random-init bf16, batch 1, "
+                                      "640-token prompt, 256 greedy steps", **res}))
+        return
     t_setup = time.perf_counter()
     layers = make_layers(a.layers, dev)
     torch.cuda.synchronize()

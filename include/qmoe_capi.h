@@ -249,6 +249,30 @@ int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf
                      int64_t S_max, float scale, float* partial, qmoe_bf16* out,
                      qmoe_stream_t stream);
 
+/* Token embedding gather into the fp32 residual stream:
+ *   out[i, :] = float(table[ids[i], :]);  table: bf16 [V, H]; ids: i64 [n];
+ *   out: f32 [n, H].  An id outside [0, V) writes a zero row and sets
+ *   err[0] = 1 (err: i32, cleared by the caller); nothing traps on the GPU.
+ *   Limits: H % 4 == 0.
+ * Replaces: the model's ParallelEmbedding lookup (qwen_with_nki.py:10250-10256)
+ *   and the NKI embedding gather _nki_embedding_kernel (1541-1578). */
+int qmoe_embed(const qmoe_bf16* table, int64_t V, int64_t H, const int64_t* ids, int64_t n,
+               float* out, int32_t* err, qmoe_stream_t stream);
+
+/* Greedy token per row: out[r] = argmax_j x[r, j] (first maximum; NaN ranks
+ * highest, first NaN wins), in two launches with no memset, so it replays
+ * correctly inside a HIP graph.  x: f32 rows of n (row stride ldx); out: i64
+ * [rows]; workspace of qmoe_argmax_workspace(rows) bytes.
+ * Replaces: greedy selection over the lm_head logits in the generation loop
+ *   (main.py:557-569 with do_sample off; the reference's on-device sampling
+ *   path and _nki_lm_head_kernel 1766-1805 produce the logits it reads). */
+int qmoe_argmax(const float* x, int64_t rows, int64_t n, int64_t ldx, void* workspace,
+                int64_t workspace_bytes, int64_t* out, qmoe_stream_t stream);
+
+/* Workspace bytes of qmoe_argmax for `rows` rows (-1 for rows < 0).
+ * Replaces: nothing in the reference; the caller owns memory here. */
+int64_t qmoe_argmax_workspace(int64_t rows);
+
 #ifdef __cplusplus
 }
 #endif

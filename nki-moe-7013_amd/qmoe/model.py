@@ -182,6 +182,8 @@ class NeuronQwen3MoeModel:
         dev = self.embed_tokens.device
         max_pos = min(int(config.max_position_embeddings), int(config.neuron_config.max_length) + 1)
         self.rope = rope_tables(config.head_dim, max_pos, float(config.rope_theta), dev)
+        # set by the embedding gather when a token id is outside the vocabulary
+        self.embed_err = torch.zeros(1, dtype=torch.int32, device=dev)
 
     def allocate_cache(self, B: int, S_max: int):
         c = self.config
@@ -191,15 +193,16 @@ class NeuronQwen3MoeModel:
     def hidden(self, input_ids: torch.Tensor, positions: torch.Tensor, B: int, S: int, start: int,
                ctx_len: Optional[torch.Tensor] = None, h_buf: Optional[torch.Tensor] = None) -> torch.Tensor:
         """fp32 final hidden states ``[B*S, H]`` (before the final norm)."""
-        emb = torch.nn.functional.embedding(input_ids.reshape(-1), self.embed_tokens)
-        if h_buf is None:
-            h = emb.float()
-        else:
-            h = h_buf
-            h.copy_(emb)
+        h = ops.embed(input_ids.reshape(-1).long(), self.embed_tokens, out=h_buf, err=self.embed_err)
         for layer in self.layers:
             layer.run(h, positions, B, S, self.rope, start, ctx_len)
         return h
+
+    def check_embed(self) -> None:
+        """Raise if any token id so far was outside the vocabulary (synchronises)."""
+        if int(self.embed_err.item()):
+            self.embed_err.zero_()
+            raise ValueError("token id outside [0, vocab_size) reached the embedding")
 
     def logits(self, h_last: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Final RMSNorm + lm_head (fp32 accumulation) on rows ``h_last[n, H]``."""
@@ -389,8 +392,9 @@ class NeuronQwen3MoeForCausalLM:
         if not use_graph:
             toks, cur = [], first_token.to(self.device)
             for _ in range(n_steps):
-                cur = self.decode_step(cur).argmax(dim=-1)
+                cur = ops.argmax(self.decode_step(cur))
                 toks.append(cur)
+            self.model.check_embed()
             return torch.stack(toks, dim=1)
         st = self._decode_graph(B)
         st["tok"].copy_(first_token.to(self.device).view(B).long())
@@ -400,6 +404,7 @@ class NeuronQwen3MoeForCausalLM:
             st["graph"].replay()
             out[:, i].copy_(st["tok"])
         self.position += n_steps
+        self.model.check_embed()
         return out
 
     def _decode_graph(self, B: int):
@@ -410,13 +415,17 @@ class NeuronQwen3MoeForCausalLM:
         st = {"tok": torch.zeros(B, dtype=torch.long, device=dev),
               "pos": torch.zeros(B, dtype=torch.int32, device=dev),
               "h": torch.empty(B, self.config.hidden_size, device=dev),
-              "logits": torch.empty(B, self.config.vocab_size, device=dev)}
+              "logits": torch.empty(B, self.config.vocab_size, device=dev),
+              "am_ws": ops.argmax_workspace(B, dev)}
 
+        # Every op of the step is a library kernel or an elementwise torch op:
+        # no reduction that records a memset into the graph (torch's argmax
+        # over a 151,936-wide row would), so replays stay correct.
         def step():
             ctx = st["pos"] + 1
             h = m.hidden(st["tok"].view(B, 1), st["pos"], B, 1, 0, ctx_len=ctx, h_buf=st["h"])
             m.logits(h, out=st["logits"])
-            st["tok"].copy_(st["logits"].argmax(dim=-1))
+            ops.argmax(st["logits"], out=st["tok"], workspace=st["am_ws"])
             st["pos"].add_(1)
 
         # Warm-up on a side stream (allocations, lazily created workspaces), then

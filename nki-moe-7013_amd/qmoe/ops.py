@@ -498,3 +498,52 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, c
         "qmoe_attn_decode",
     )
     return out
+
+
+# ----------------------------------------------------------------- embedding / greedy argmax
+def embed(ids: torch.Tensor, table: torch.Tensor, out: Optional[torch.Tensor] = None,
+          err: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp32 rows ``table[ids]`` (``ids`` i64, any shape; returns ``[ids.numel(), H]``).
+    Out-of-range ids give zero rows and set ``err[0] = 1`` (``err``: i32 [1],
+    cleared by the caller) instead of trapping on the GPU."""
+    if table.dim() != 2:
+        raise ValueError("table must be [V, H]")
+    V, H = table.shape
+    _need(table, "table", BF16)
+    flat = ids.reshape(-1)
+    if flat.dtype != torch.int64:
+        raise ValueError("ids must be int64")
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    n = flat.numel()
+    out = torch.empty(n, H, dtype=F32, device=table.device) if out is None else out
+    _need(out, "out", F32, (n, H))
+    if err is None:
+        err = torch.zeros(1, dtype=I32, device=table.device)
+    _need(err, "err", I32, (1,))
+    _same_device(flat, table, out, err)
+    check(lib().qmoe_embed(_ptr(table), V, H, _ptr(flat), n, _ptr(out), _ptr(err), _stream()), "qmoe_embed")
+    return out
+
+
+def argmax_workspace(rows: int, device) -> torch.Tensor:
+    n = int(lib().qmoe_argmax_workspace(rows))
+    return torch.empty(max(n, 8), dtype=torch.uint8, device=device)
+
+
+def argmax(x: torch.Tensor, out: Optional[torch.Tensor] = None,
+           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row-wise argmax of f32 ``x[rows, n]`` into i64 ``out[rows]`` (first max;
+    NaN highest) -- graph-safe (no memset, no semaphores)."""
+    if x.dim() != 2:
+        raise ValueError("x must be [rows, n]")
+    rows, n = x.shape
+    _need(x, "x", F32)
+    out = torch.empty(rows, dtype=torch.int64, device=x.device) if out is None else out
+    _need(out, "out", torch.int64, (rows,))
+    workspace = argmax_workspace(rows, x.device) if workspace is None else workspace
+    _need(workspace, "workspace", torch.uint8)
+    _same_device(x, out, workspace)
+    check(lib().qmoe_argmax(_ptr(x), rows, n, n, _ptr(workspace), workspace.numel(), _ptr(out), _stream()),
+          "qmoe_argmax")
+    return out

@@ -52,6 +52,10 @@ def test_version():
         (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2048, 100, 128, 8, 1, 1, None), "I % 128"),
         (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2176, 768, 128, 8, 1, 1, None), "H % 256"),
         (lambda l: l.qmoe_moe_combine(1, 0, 1, 1, None, 4, 8, 6, 1, None), "H % 4"),
+        (lambda l: l.qmoe_embed(1, 100, 6, 1, 1, 1, 1, None), "H % 4 == 0"),
+        (lambda l: l.qmoe_embed(None, 100, 8, 1, 1, 1, 1, None), "null pointer"),
+        (lambda l: l.qmoe_argmax(1, 2, 100, 100, 1, 8, 1, None), "workspace too small"),
+        (lambda l: l.qmoe_argmax(1, 2, 100, 50, 1, 1 << 20, 1, None), "bad rows/n/ldx"),
         # decode block: x, h, rms_w, eps, w_router, bias, w13, w2, residual, T, H, I, E, k,
         #   logits, topk_idx, topk_w, workspace, workspace_bytes, x_out, out, stream
         (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 768, 128, 8,

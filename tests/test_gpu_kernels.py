@@ -458,3 +458,69 @@ def test_moe_decode_block(dev, experts, router_w, T, normed):
     rows = [t for t in range(T) if bool(ok[t])]
     ref = _oracle_rows(xin, ri, rw, _ExpertCache(w13, w2), rows)
     assert_close_layer(outs[0].cpu()[rows] - residual.cpu()[rows], ref, f"decode block T={T}", 2e-3, 1e-4)
+
+
+# --------------------------------------------------------------------------- embedding / greedy argmax
+def test_embed_gather_and_bad_ids(dev):
+    announce("embedding gather")
+    g = torch.Generator(device=dev).manual_seed(3)
+    V, Hh = 1000, 2048
+    table = bf16_randn((V, Hh), g, dev)
+    ids = torch.tensor([0, 999, 17, 17, 512], dtype=torch.int64, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = ops.embed(ids, table, err=err)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), table.cpu()[ids.cpu()].float())
+    assert int(err.item()) == 0
+    bad = torch.tensor([3, -1, V, 4], dtype=torch.int64, device=dev)
+    out = ops.embed(bad, table, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    assert float(out[1].abs().sum()) == 0.0 and float(out[2].abs().sum()) == 0.0
+    assert torch.equal(out.cpu()[[0, 3]], table.cpu()[[3, 4]].float())
+
+
+def test_argmax_rows_match_torch(dev):
+    announce("argmax rows")
+    g = torch.Generator(device=dev).manual_seed(4)
+    n = 151936
+    x = torch.randn(4, n, generator=g, device=dev)
+    x[1, 777] = 50.0
+    x[1, 99999] = 50.0  # tie: the lower index wins
+    x[2, 1234] = float("nan")
+    x[2, 5] = float("nan")  # first NaN wins
+    x[3] = -float("inf")
+    x[3, n - 1] = -1e30
+    got = ops.argmax(x)
+    torch.cuda.synchronize()
+    assert got.cpu().tolist() == [int(x[0].cpu().argmax()), 777, 5, n - 1]
+    y = torch.randn(7, 300, generator=g, device=dev)
+    assert torch.equal(ops.argmax(y).cpu(), y.cpu().argmax(dim=-1))
+
+
+def test_argmax_graph_replays(dev):
+    """Captured argmax over a vocabulary-wide row, replayed with fresh data
+    (written eagerly between replays): every replay equals torch.argmax."""
+    announce("argmax in a HIP graph")
+    g = torch.Generator(device=dev).manual_seed(5)
+    n = 151936
+    x = torch.empty(1, n, device=dev)
+    out = torch.zeros(1, dtype=torch.int64, device=dev)
+    ws = ops.argmax_workspace(1, dev)
+    x.normal_(generator=g)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.argmax(x, out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.argmax(x, out=out, workspace=ws)
+    for i in range(6):
+        x.normal_(generator=g)
+        x[0, (i * 7919) % n] = 100.0 + i
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(out.item()) == (i * 7919) % n == int(x.cpu().argmax())
