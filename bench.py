@@ -54,11 +54,13 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--extra", action="store_true",
-                    help="also time T=8/64 decode, T=4096 prefill and the attention layer")
+                    help="also time T=8/64 decode and the attention layer")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC traffic runs")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--model", action="store_true",
-                    help="also time the full 48-layer model (TTFT at 640 tokens, 256 greedy steps)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the T=4096 prefill MoE block")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the full 48-layer model (TTFT at 640 tokens, 256 greedy steps; "
+                         "run in a child process)")
     ap.add_argument("--only-model", action="store_true",
                     help="time only the full model, in this process, and print its numbers as JSON")
     return ap.parse_args()
@@ -313,6 +315,20 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     }
 
 
+def model_child():
+    """The full-model numbers from ``bench.py --only-model`` in a child process
+    (its own 61 GB of weights; this process keeps its MoE layers)."""
+    cmd = [sys.executable, os.path.abspath(__file__), "--only-model"]
+    try:
+        r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return {"error": "timed out"}
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"error": f"exit {r.returncode}", "stderr_tail": r.stderr[-400:]}
+    return json.loads(lines[-1])
+
+
 CAL_ELEMS = 64 << 20  # bf16 elements of the calibration kernel (128 MiB in, 128 MiB out)
 
 
@@ -461,21 +477,18 @@ def main():
     dec = bench_decode(layers, a.tokens, a.steps, a.warmup, dev)
     print(f"[bench] decode T={a.tokens}: {dec}", file=sys.stderr, flush=True)
     extra = {}
+    if not a.no_prefill:
+        extra["prefill_T4096"] = bench_prefill(layers, dev)
+        print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
     if a.extra:
         for T in (8, 64):
             extra[f"decode_T{T}"] = bench_decode(layers, T, 480, 48, dev)
             print(f"[bench] decode T={T}: {extra[f'decode_T{T}']}", file=sys.stderr, flush=True)
-        extra["prefill_T4096"] = bench_prefill(layers, dev)
-        print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
         extra["attention_B8"] = bench_attention(dev)
         print(f"[bench] attention: {extra['attention_B8']}", file=sys.stderr, flush=True)
-    if a.model:
-        cpu_layer = layers[0]
-        del layers[1:]
-        torch.cuda.empty_cache()
-        extra["model_48L"] = bench_model(dev)
+    if not a.no_model:
+        extra["model_48L"] = model_child()
         print(f"[bench] model: {extra['model_48L']}", file=sys.stderr, flush=True)
-        layers = [cpu_layer]
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -505,6 +518,20 @@ def main():
         },
         "moe_block_GBps": round(dec["block_GBps"], 1),
         "moe_block_hbm_frac": round(dec["block_frac"], 4),
+        # the north-star companions: prefill MoE block (T=4096, Zipf-skewed
+        # routing) and the full 48-layer model at batch 1 (child process)
+        "prefill_moe_block_tokens_per_s": (round(extra["prefill_T4096"]["tokens_per_s"], 1)
+                                           if "prefill_T4096" in extra else None),
+        "prefill_experts_mfma_frac": (round(extra["prefill_T4096"]["experts_mfma_frac"], 4)
+                                      if "prefill_T4096" in extra else None),
+        "model_decode_tokens_per_s": (round(extra["model_48L"]["decode_tokens_per_s"], 2)
+                                      if "decode_tokens_per_s" in extra.get("model_48L", {}) else None),
+        "model_decode_hbm_frac": (round(extra["model_48L"]["decode_GBps"] / HBM_PEAK_GBS, 4)
+                                  if "decode_GBps" in extra.get("model_48L", {}) else None),
+        "model_ttft_ms": (round(extra["model_48L"]["ttft_ms"], 3)
+                          if "ttft_ms" in extra.get("model_48L", {}) else None),
+        "model_prefill_tokens_per_s": (round(extra["model_48L"]["prefill_tokens_per_s"], 1)
+                                       if "prefill_tokens_per_s" in extra.get("model_48L", {}) else None),
         "roofline": {
             "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
                        "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else
