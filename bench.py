@@ -184,7 +184,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     import torch
 
     from qmoe import ops
-    from qmoe.moe import MoEBlock
+    from qmoe.moe import MoEBlock, TILE_M
 
     g = torch.Generator(device=dev).manual_seed(77)
     rank = torch.randperm(E, generator=torch.Generator().manual_seed(5)).float() + 1.0
@@ -206,7 +206,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     routes = []
     for l in range(L):
         _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
-        routes.append(ops.moe_permute(ti, E, 128))
+        routes.append(ops.moe_permute(ti, E, TILE_M))
 
     def run_experts(i):
         l = i % L

@@ -50,6 +50,9 @@ typedef void* qmoe_stream_t;
  * 8-unit slice of one expert's down matrix is one contiguous H x 16-byte run. */
 #define QMOE_W2_BLOCK 8
 
+/* Largest row tile (tile_m of qmoe_moe_permute) qmoe_moe_experts_grouped takes. */
+#define QMOE_GROUPED_MAX_TILE_M 256
+
 /* Workgroups of the decode block's expert kernel (one per MI355X CU); sets
  * the size of its partial-output workspace. */
 #define QMOE_DECODE_BLOCK_WGS 256
@@ -162,7 +165,10 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   act[s]    = bf16(silu(x[tok(s)] . Wg[e]^T) * (x[tok(s)] . Wu[e]^T))
  *   y_slot[s] = bf16(act[s] . W2[e]^T)
  *   x: bf16 [T, H]; w13: bf16 [E, 2I, H] packed; w2: bf16 [E, I/8, H, 8] blocked;
- *   slot_token/tiles/meta from qmoe_moe_permute with tile_m == 128;
+ *   slot_token/tiles/meta from qmoe_moe_permute with tile_m <=
+ *   QMOE_GROUPED_MAX_TILE_M (256 is the efficient choice: every tile is one
+ *   256 x 256 MFMA tile, partial tiles run only their live 32-row blocks);
+ *   max_tiles >= ceil(T*k / QMOE_GROUPED_MAX_TILE_M) + E (the grid size);
  *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
  *   Limits: H % 256 == 0, I % 128 == 0; x, act and one expert's w13 each
  *   below 2 GiB.

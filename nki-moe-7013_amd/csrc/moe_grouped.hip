@@ -1,35 +1,58 @@
 // Prefill-shape expert MLPs as two grouped GEMMs on bf16 MFMA.
 //
-// The row-tile table from qmoe_moe_permute (tile_m = 128) lists, for every
-// expert, runs of at most 128 expert-sorted slots.  Each workgroup takes one
-// (row tile, 256-column tile) pair on the direct-to-LDS pipeline
-// (mfma_pipe.hpp, 128 x 256 x 32, three stages: 72 KB of LDS and at most 256
-// registers, so two workgroups share a CU and one's prologue and epilogue
-// overlap the other's MFMAs):
+// The row-tile table from qmoe_moe_permute (tile_m <= 256) lists, for every
+// expert, runs of at most 256 expert-sorted slots.  Each workgroup takes one
+// (row tile, 256-row weight panel) pair on the direct-to-LDS pipeline of
+// mfma_wide.hpp (512 threads; A = 256 weight rows, B = up to 256 tokens; one
+// workgroup per CU).  Two pipelines share the grid, chosen per tile:
+//   - more than 64 live rows: 256 x 256 x 32 stages, three deep, only the
+//     live 32-row token blocks computed;
+//   - at most 64 live rows (cold experts, where streaming the weights is the
+//     whole cost): 256 x 64 x 64 stages, four deep, so three 32 KB weight
+//     slabs are in flight and one barrier covers 64 columns of K.
 //
-//   gate_up:  A rows gathered on load from x[slot_token[s]] (no permuted copy
-//             of X; rows past the tile's run read as zeros), B = 256 packed
-//             rows of w13[e].  The packed layout puts 32 gate rows next to
-//             their 32 up rows, so each wave's column blocks pair up as
-//             (gate, up) in the same lane and register: the SwiGLU epilogue
-//             act = bf16(silu(g) * u) is elementwise, fp32 before the cast.
-//   down:     A rows = act[s] (already contiguous in slot order),
-//             B = 256 rows h of w2[e] in the blocked layout [I/8][H][8]: the
+//   gate_up:  A = 256 packed rows of w13[e] (32 gate rows next to their 32 up
+//             rows), B rows gathered on load from x[slot_token[s]] (no
+//             permuted copy of X; rows past the run read as zeros).  A wave's
+//             two A blocks are one gate block and its up block, so the SwiGLU
+//             epilogue act = bf16(silu(g) * u) is elementwise in fp32.
+//   down:     A = 256 rows h of w2[e] in the blocked layout [I/8][H][8]: the
 //             16-byte chunk (h, k..k+7) sits at ((k/8)*H + h)*16, so a stage
-//             of BK = 32 columns is 4 chunks of every row, BK/8*H*16 bytes
-//             further on per stage; the epilogue writes y_slot[s] in bf16.
+//             of BK columns is BK/8 chunks of every row, BK/8*H*16 bytes
+//             further on per stage; B = act[s] (contiguous in slot order).
+//   Both epilogues stage the bf16 tile through LDS (rows padded by 16 bytes)
+//   and write whole 16-byte chunks of contiguous output rows.
 //
-// Grid: one workgroup per (tile, column tile) up to max_tiles; the live ones
-// (tile < meta[0]) are renumbered XCD-contiguously, column tiles fastest, so
-// one XCD works through consecutive tiles (mostly one expert at a time) and
-// its L2 holds that expert's weight panels and the tiles' token rows.
-#include "mfma_pipe.hpp"
+// Grid: one workgroup per (tile, panel) up to max_tiles; the live ones
+// (tile < meta[0]) are renumbered XCD-contiguously, panels fastest, so one
+// XCD works through consecutive tiles (mostly one expert at a time) and its
+// L2 serves that expert's weight panels and the tiles' token rows to all of
+// them.
+#include "mfma_wide.hpp"
 
 namespace qmoe {
 
 namespace {
-using GP = pipe::Pipe<128, 256, 32, 3>;
-static_assert(GP::BK % QMOE_W2_BLOCK == 0, "a stage covers whole w2 blocks");
+// Full and partial tiles (more than 64 live rows): 256 x 256 x 32, three
+// stages, 8 waves (2 per SIMD) of 64 x 128.
+using Hot = pipe::Wide<4, 2, 32, 3, 256>;
+// Cold tiles (at most 64 live rows: weight streaming dominates): 256 x 64 x 64,
+// four stages, so three 32 KB weight slabs are in flight and a barrier covers
+// 64 columns of K.
+using Cold = pipe::Wide<4, 2, 64, 4, 64>;
+constexpr int COLD_MAX_ROWS = Cold::BN;
+constexpr int PIPE_SMEM = Hot::SMEM > Cold::SMEM ? Hot::SMEM : Cold::SMEM;
+constexpr int PANEL = Hot::BM;
+static_assert(Hot::BM == Cold::BM && Hot::THREADS == Cold::THREADS, "one grid for both pipelines");
+static_assert(Cold::BK % QMOE_W2_BLOCK == 0 && Hot::BK % QMOE_W2_BLOCK == 0, "a stage covers whole w2 blocks");
+static_assert(PANEL % (2 * QMOE_W13_GROUP) == 0 && QMOE_W13_GROUP == 32,
+              "a wave's 64 packed w13 rows are one gate block and its up block");
+
+// Epilogue staging rows (bf16 elements): PANEL/2 act units or PANEL y columns + 16 B.
+constexpr int ACT_LD = PANEL / 2 + 8, Y_LD = PANEL + 8;
+constexpr int EPI_SMEM = Hot::BN * Y_LD * 2;
+constexpr int SMEM = PIPE_SMEM > EPI_SMEM ? PIPE_SMEM : EPI_SMEM;
+static_assert(SMEM <= 160 * 1024, "LDS");
 
 struct TileJob {
   int e, s0, rows, n0;
@@ -37,91 +60,146 @@ struct TileJob {
 
 // Returns false for a workgroup beyond the live tiles.
 __device__ __forceinline__ bool tile_job(const int32_t* __restrict__ tiles,
-                                         const int32_t* __restrict__ meta, int ncols, TileJob& job) {
-  const int live = meta[0] * ncols;
+                                         const int32_t* __restrict__ meta, int npanels, TileJob& job) {
+  const int live = meta[0] * npanels;
   const int hw = int(blockIdx.x);
   if (hw >= live) return false;
   const int item = pipe::xcd_contiguous(hw, live);
-  const int t = item / ncols;
-  job.n0 = (item - t * ncols) * GP::BN;
+  const int t = item / npanels;
+  job.n0 = (item - t * npanels) * PANEL;
   job.e = tiles[4 * t];
   job.s0 = tiles[4 * t + 1];
-  job.rows = tiles[4 * t + 2] - job.s0;
+  job.rows = min(tiles[4 * t + 2] - job.s0, Hot::BN);
   return true;
+}
+
+__device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) {
+  return make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
+}
+
+template <class P>
+__device__ __forceinline__ void gateup_tile(const TileJob& job, const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ w13,
+                                            const int32_t* __restrict__ slot_token, int T, int H, int I,
+                                            uint16_t* __restrict__ act, uint8_t* smem) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const pipe::i32x4 ra = pipe::make_rsrc(w13 + int64_t(job.e) * 2 * I * H, uint32_t(int64_t(2) * I * H * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(x, uint32_t(int64_t(T) * H * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int r = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(r, lane);
+    if (j < P::AI)
+      vo[j] = uint32_t(job.n0 + r) * uint32_t(H * 2) + c;
+    else
+      vo[j] = r < job.rows ? uint32_t(slot_token[job.s0 + r]) * uint32_t(H * 2) + c : pipe::PAD;
+  }
+  const int nbw = P::wave_blocks(wave, (job.rows + 31) / 32);
+  typename P::Acc acc;
+  P::run_dyn(nbw, ra, rb, vo, H / P::BK, smem, acc, uint32_t(P::BK * 2), uint32_t(P::BK * 2));
+  // A block 0 = gate rows, block 1 = up rows of units n0/2 + 32 wm + [0, 32).  The
+  // tile goes through LDS ([token][128 units], rows padded to 272 B) so that the
+  // global stores are whole 16-byte chunks of contiguous act rows.
+  __syncthreads();  // every wave is past its last fragment read
+  uint16_t* tl = reinterpret_cast<uint16_t*>(smem);
+  const int u_wave = P::wave_arow(wave) / 2 + (lane >> 5) * 4;  // FM/2 (gate, up) block pairs per wave
+#pragma unroll
+  for (int j = 0; j < P::FN; ++j) {
+    if (j >= nbw) break;
+    const int tok = P::acc_brow(wave, j, lane);
+#pragma unroll
+    for (int p = 0; p < P::FM / 2; ++p) {
+      const f32x16& g = acc[2 * p][j];
+      const f32x16& u = acc[2 * p + 1][j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint2*>(tl + tok * ACT_LD + u_wave + p * 32 + q * 8) =
+            pack4_bf16(silu(g[4 * q]) * u[4 * q], silu(g[4 * q + 1]) * u[4 * q + 1],
+                       silu(g[4 * q + 2]) * u[4 * q + 2], silu(g[4 * q + 3]) * u[4 * q + 3]);
+    }
+  }
+  __syncthreads();
+  uint16_t* dst = act + int64_t(job.s0) * I + job.n0 / 2;
+  for (int c = threadIdx.x; c < job.rows * (PANEL / 16); c += P::THREADS) {
+    const int r = c / (PANEL / 16), k = c % (PANEL / 16);
+    *reinterpret_cast<uint4*>(dst + int64_t(r) * I + k * 8) = *reinterpret_cast<const uint4*>(tl + r * ACT_LD + k * 8);
+  }
+}
+
+template <class P>
+__device__ __forceinline__ void down_tile(const TileJob& job, const uint16_t* __restrict__ act,
+                                          const uint16_t* __restrict__ w2, int slots, int H, int I,
+                                          uint16_t* __restrict__ y_slot, uint8_t* smem) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const pipe::i32x4 ra = pipe::make_rsrc(w2 + int64_t(job.e) * H * I, uint32_t(int64_t(H) * I * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(act, uint32_t(int64_t(slots) * I * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int r = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(r, lane);
+    if (j < P::AI)  // chunk index c/16 of this stage = k block; rows h contiguous within a block
+      vo[j] = ((c / 16) * uint32_t(H) + uint32_t(job.n0 + r)) * 16u;
+    else
+      vo[j] = r < job.rows ? uint32_t(job.s0 + r) * uint32_t(I * 2) + c : pipe::PAD;
+  }
+  const int nbw = P::wave_blocks(wave, (job.rows + 31) / 32);
+  typename P::Acc acc;
+  P::run_dyn(nbw, ra, rb, vo, I / P::BK, smem, acc, uint32_t(P::BK / QMOE_W2_BLOCK) * uint32_t(H) * 16u,
+             uint32_t(P::BK * 2));
+  // Through LDS ([token][256 h], rows padded to 528 B), then 16-byte row chunks.
+  __syncthreads();
+  uint16_t* tl = reinterpret_cast<uint16_t*>(smem);
+  const int h_local = P::wave_arow(wave) + (lane >> 5) * 4;
+#pragma unroll
+  for (int j = 0; j < P::FN; ++j) {
+    if (j >= nbw) break;
+    const int tok = P::acc_brow(wave, j, lane);
+#pragma unroll
+    for (int i = 0; i < P::FM; ++i) {
+      const f32x16& a = acc[i][j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint2*>(tl + tok * Y_LD + h_local + i * 32 + q * 8) =
+            pack4_bf16(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    }
+  }
+  __syncthreads();
+  uint16_t* dst = y_slot + int64_t(job.s0) * H + job.n0;
+  for (int c = threadIdx.x; c < job.rows * (PANEL / 8); c += P::THREADS) {
+    const int r = c / (PANEL / 8), k = c % (PANEL / 8);
+    *reinterpret_cast<uint4*>(dst + int64_t(r) * H + k * 8) = *reinterpret_cast<const uint4*>(tl + r * Y_LD + k * 8);
+  }
 }
 }  // namespace
 
-__global__ __launch_bounds__(256, 2) void moe_gateup_grouped_kernel(
+__global__ __launch_bounds__(Hot::THREADS, 1) void moe_gateup_grouped_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w13,
     const int32_t* __restrict__ slot_token, const int32_t* __restrict__ tiles,
     const int32_t* __restrict__ meta, int T, int H, int I, uint16_t* __restrict__ act) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   TileJob job;
-  if (!tile_job(tiles, meta, 2 * I / GP::BN, job)) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const pipe::i32x4 ra = pipe::make_rsrc(x, uint32_t(int64_t(T) * H * 2));
-  const pipe::i32x4 rb = pipe::make_rsrc(w13 + int64_t(job.e) * 2 * I * H, uint32_t(int64_t(2) * I * H * 2));
-  uint32_t vo[GP::NDMA];
-#pragma unroll
-  for (int j = 0; j < GP::NDMA; ++j) {
-    const int r = GP::dma_row(j, wave, lane);
-    const uint32_t c = GP::dma_chunk(r, lane);
-    if (j < GP::AI)
-      vo[j] = r < job.rows ? uint32_t(slot_token[job.s0 + r]) * uint32_t(H * 2) + c : pipe::PAD;
-    else
-      vo[j] = uint32_t(job.n0 + r) * uint32_t(H * 2) + c;
-  }
-  GP::Acc acc;
-  GP::run(ra, rb, vo, H / GP::BK, smem, acc);
-  // column blocks (2p, 2p+1) = gate / up rows of units n0/2 + wn*64 + p*32 + [0, 32)
-  const int unit0 = job.n0 / 2 + (wave & 1) * (GP::WN / 2) + (lane & 31);
-#pragma unroll
-  for (int i = 0; i < GP::FM; ++i)
-#pragma unroll
-    for (int p = 0; p < GP::FN / 2; ++p)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = GP::acc_row(wave, i, e, lane);
-        if (row < job.rows) {
-          const float g = acc[i][2 * p][e], u = acc[i][2 * p + 1][e];
-          act[int64_t(job.s0 + row) * I + unit0 + p * 32] = f32_to_bf16(silu(g) * u);
-        }
-      }
+  if (!tile_job(tiles, meta, 2 * I / PANEL, job)) return;
+  if (job.rows <= COLD_MAX_ROWS)
+    gateup_tile<Cold>(job, x, w13, slot_token, T, H, I, act, smem);
+  else
+    gateup_tile<Hot>(job, x, w13, slot_token, T, H, I, act, smem);
 }
 
-__global__ __launch_bounds__(256, 2) void moe_down_grouped_kernel(
+__global__ __launch_bounds__(Hot::THREADS, 1) void moe_down_grouped_kernel(
     const uint16_t* __restrict__ act, const uint16_t* __restrict__ w2,
     const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, int slots, int H, int I,
     uint16_t* __restrict__ y_slot) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   TileJob job;
-  if (!tile_job(tiles, meta, H / GP::BN, job)) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const pipe::i32x4 ra = pipe::make_rsrc(act, uint32_t(int64_t(slots) * I * 2));
-  const pipe::i32x4 rb = pipe::make_rsrc(w2 + int64_t(job.e) * H * I, uint32_t(int64_t(H) * I * 2));
-  uint32_t vo[GP::NDMA];
-#pragma unroll
-  for (int j = 0; j < GP::NDMA; ++j) {
-    const int r = GP::dma_row(j, wave, lane);
-    const uint32_t c = GP::dma_chunk(r, lane);
-    if (j < GP::AI)
-      vo[j] = r < job.rows ? uint32_t(job.s0 + r) * uint32_t(I * 2) + c : pipe::PAD;
-    else  // chunk index c/16 of this stage = k block; rows h contiguous within a block
-      vo[j] = ((c / 16) * uint32_t(H) + uint32_t(job.n0 + r)) * 16u;
-  }
-  GP::Acc acc;
-  GP::run(ra, rb, vo, I / GP::BK, smem, acc, uint32_t(GP::BK / QMOE_W2_BLOCK) * uint32_t(H) * 16u);
-#pragma unroll
-  for (int i = 0; i < GP::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < GP::FN; ++j) {
-      const int col = job.n0 + GP::acc_col(wave, j, lane);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = GP::acc_row(wave, i, e, lane);
-        if (row < job.rows) y_slot[int64_t(job.s0 + row) * H + col] = f32_to_bf16(acc[i][j][e]);
-      }
-    }
+  if (!tile_job(tiles, meta, H / PANEL, job)) return;
+  if (job.rows <= COLD_MAX_ROWS)
+    down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
+  else
+    down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
 }
 
 }  // namespace qmoe
@@ -142,24 +220,24 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
   // every buffer the DMA reads must stay below 2 GiB (32-bit offsets, PAD above)
   QMOE_REQUIRE(T * H * 2 < (1ll << 31) && T * k * I * 2 < (1ll << 31) && 2 * I * H * 2 < (1ll << 31),
                "qmoe_moe_experts_grouped: operand larger than 2 GiB");
-  QMOE_REQUIRE(max_tiles >= (T * k + 127) / 128 + E && max_tiles < (1 << 20),
-               "qmoe_moe_experts_grouped: max_tiles must be in [ceil(T*k/128)+E, 2^20)");
+  QMOE_REQUIRE(max_tiles >= (T * k + 255) / 256 + E && max_tiles < (1 << 20),
+               "qmoe_moe_experts_grouped: max_tiles must be in [ceil(T*k/256)+E, 2^20)");
   if (T == 0) return QMOE_OK;
   static const bool attr = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(moe_gateup_grouped_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, GP::SMEM);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(moe_down_grouped_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, GP::SMEM);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
     return true;
   }();
   (void)attr;
   hipStream_t s = as_stream(stream);
-  const unsigned g1 = unsigned(max_tiles * (2 * I / GP::BN)), g2 = unsigned(max_tiles * (H / GP::BN));
-  hipLaunchKernelGGL(moe_gateup_grouped_kernel, dim3(g1), dim3(256), GP::SMEM, s, x, w13, slot_token,
+  const unsigned g1 = unsigned(max_tiles * (2 * I / PANEL)), g2 = unsigned(max_tiles * (H / PANEL));
+  hipLaunchKernelGGL(moe_gateup_grouped_kernel, dim3(g1), dim3(Hot::THREADS), SMEM, s, x, w13, slot_token,
                      tiles, meta, int(T), int(H), int(I), act);
   int rc = hip_status("qmoe_moe_experts_grouped(gate_up)");
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_down_grouped_kernel, dim3(g2), dim3(256), GP::SMEM, s, act, w2, tiles, meta,
+  hipLaunchKernelGGL(moe_down_grouped_kernel, dim3(g2), dim3(Hot::THREADS), SMEM, s, act, w2, tiles, meta,
                      int(T * k), int(H), int(I), y_slot);
   return hip_status("qmoe_moe_experts_grouped(down)");
 }

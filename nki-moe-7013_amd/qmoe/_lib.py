@@ -21,6 +21,7 @@ GEMM_ADD_F32 = 2
 
 W13_GROUP = 32
 W2_BLOCK = 8
+GROUPED_MAX_TILE_M = 256
 DECODE_BLOCK_WGS = 256
 
 P = c_void_p

@@ -18,12 +18,13 @@ from typing import Optional
 
 import torch
 
-from . import ops
+from . import _lib, ops
 
 # Token counts at or below this use the HBM-bound GEMV experts; above it the
 # MFMA grouped GEMM.  (Each touched expert is streamed once either way.)
 GEMV_MAX_TOKENS = 64
-TILE_M = 128
+# Row tile of the prefill dispatch table: one 256 x 256 MFMA tile per (tile, panel).
+TILE_M = _lib.GROUPED_MAX_TILE_M
 
 
 class ExpertMLPs:

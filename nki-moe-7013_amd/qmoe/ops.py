@@ -319,8 +319,8 @@ def moe_experts_grouped(
 ) -> torch.Tensor:
     """Prefill-shape experts (MFMA); returns unweighted ``y_slot[T*k, H]`` (bf16)."""
     T, H, I, E = _check_experts(x, w13, w2)
-    if (route.T, route.E) != (T, E) or route.tile_m != 128:
-        raise ValueError("route must match x / w13 and use tile_m=128")
+    if (route.T, route.E) != (T, E) or not 0 < route.tile_m <= _lib.GROUPED_MAX_TILE_M:
+        raise ValueError(f"route must match x / w13 and use tile_m <= {_lib.GROUPED_MAX_TILE_M}")
     k = route.k
     dev = x.device
     act = torch.empty(T * k, I, dtype=BF16, device=dev) if act is None else act

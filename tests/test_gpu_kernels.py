@@ -218,7 +218,7 @@ def test_experts_and_combine(dev, experts, T):
     tw = torch.rand(T, K_TOP, generator=g, device=dev)
     tw = tw / tw.sum(-1, keepdim=True)
     residual = torch.randn(T, H, generator=g, device=dev)
-    route = ops.moe_permute(top, E, 128)
+    route = ops.moe_permute(top, E, 256)
     y = ops.moe_experts_gemv(x, w13, w2, route) if T <= 64 else ops.moe_experts_grouped(x, w13, w2, route)
     out = ops.moe_combine(y, route, tw, residual=residual)
     torch.cuda.synchronize()
@@ -231,6 +231,23 @@ def test_experts_and_combine(dev, experts, T):
                        mean_rel_tol=1e-4 if tight else 5e-3)
 
 
+@pytest.mark.parametrize("tile_m", [32, 128])
+def test_experts_grouped_small_tiles(dev, experts, tile_m):
+    """Grouped experts take any tile table with runs of at most 256 rows: a
+    32- or 128-row table gives the same bf16 y_slot bits as the 256-row one
+    (each output element is one K-ordered MFMA chain either way)."""
+    announce(f"grouped experts tile_m={tile_m} vs 256")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(3)
+    T = 700
+    x = bf16_randn((T, H), g, dev)
+    top = torch.from_numpy(_random_topk(T, K_TOP, E, 3, skew=1.1)).to(dev)
+    y_ref = ops.moe_experts_grouped(x, w13, w2, ops.moe_permute(top, E, 256))
+    y = ops.moe_experts_grouped(x, w13, w2, ops.moe_permute(top, E, tile_m))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+
+
 def test_experts_deterministic(dev, experts):
     announce("experts repeat-run bitwise equality T=512")
     w13, w2 = experts
@@ -241,7 +258,7 @@ def test_experts_deterministic(dev, experts):
     tw = torch.full((T, K_TOP), 1.0 / K_TOP, device=dev)
     outs = []
     for _ in range(2):
-        route = ops.moe_permute(top, E, 128)
+        route = ops.moe_permute(top, E, 256)
         y = ops.moe_experts_grouped(x, w13, w2, route)
         outs.append(ops.moe_combine(y, route, tw))
     torch.cuda.synchronize()
