@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ====================================================================== decode
-constexpr int AD_SPLIT = 256;           // keys per workgroup
+constexpr int AD_SPLIT = 64;            // keys per workgroup (one wave: spreads the K/V stream over many CUs)
 constexpr int AD_WKEYS = 64;            // keys per wave; one partial (m, l, o) per wave
 constexpr int AD_SUBS = AD_SPLIT / AD_WKEYS;
 constexpr int AD_MAX_G = 16;            // q heads per kv head
@@ -310,9 +310,12 @@ constexpr int AD_PSTR = HD + 4;         // partial record: m, l, 2 pad, o[HD] (1
 // reads above the writes).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Workgroup = (256-key split, kv head, batch row); each of its four waves
-// owns 64 keys and all G q heads of the group and writes its own partial
-// (m, l, o), so no wave waits on another.  Per wave, on v_mfma_f32_32x32x16_bf16:
+// Workgroup = (AD_SPLIT-key split, kv head, batch row); each of its
+// AD_SUBS waves owns 64 keys and all G q heads of the group and writes its
+// own partial (m, l, o), so no wave waits on another.  One wave per
+// workgroup: a batch-1 step has only ctx/64 x Hkv waves of work, and each
+// CU moves a limited number of bytes per microsecond, so the K/V reads are
+// spread over as many CUs as there are waves.  Per wave, on v_mfma_f32_32x32x16_bf16:
 //   S^T [64 keys x 32] = K [64 x 128] . Q^T [128 x 32]   (q heads in columns
 //       0..G-1; K rows loaded from the cache straight into A-operand registers)
 //   softmax over keys per column: lane l holds column l % 32, 32 keys; one
@@ -321,7 +324,7 @@ __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcn
 //       this wave's LDS)
 // Every global load of the wave is issued first (K, V, q), so a split costs
 // one HBM round trip.
-__global__ __launch_bounds__(256) void attn_decode_split_kernel(
+__global__ __launch_bounds__(AD_SUBS * 64) void attn_decode_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len, int Hq, int Hkv,
     int S_max, int nsub, float scale, float* __restrict__ partial) {
@@ -593,7 +596,7 @@ extern "C" int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   const int nsub = nsplit * AD_SUBS;
   hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL(attn_decode_split_kernel, dim3(unsigned(nsplit), unsigned(Hkv), unsigned(B)),
-                     dim3(256), 0, s, q, k_cache, v_cache, ctx_len, int(Hq), int(Hkv), int(S_max), nsub,
+                     dim3(AD_SUBS * 64), 0, s, q, k_cache, v_cache, ctx_len, int(Hq), int(Hkv), int(S_max), nsub,
                      scale, partial);
   int rc = hip_status("qmoe_attn_decode(split)");
   if (rc) return rc;

@@ -264,26 +264,30 @@ static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
 template <int MT, int MODE>
 static int launch_gemv_reg(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                            void* C, int64_t ldc, hipStream_t s) {
+  // One weight row per wave for a single activation row (the most waves, each
+  // with its whole row in flight); more rows per wave amortise the staging
+  // of several activation rows.
+  constexpr int R = MT == 1 ? 1 : 4;
   const size_t shm = size_t(M) * K * 2;
   static const bool attr = [] {
-    for (const void* f : {reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 1, MODE>),
-                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 2, MODE>),
-                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 4, 4, MODE>),
-                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, 2, 8, MODE>)})
+    for (const void* f : {reinterpret_cast<const void*>(gemv_reg_kernel<MT, R, 1, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, R, 2, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, R, 4, MODE>),
+                          reinterpret_cast<const void*>(gemv_reg_kernel<MT, (R > 2 ? 2 : R), 8, MODE>)})
       (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
     return true;
   }();
   (void)attr;
   switch (K / 512) {
-#define QMOE_GR(R, KC)                                                                            \
-  case KC:                                                                                        \
-    hipLaunchKernelGGL((gemv_reg_kernel<MT, R, KC, MODE>), dim3(unsigned((N + 4 * R - 1) / (4 * R))), \
-                       dim3(256), shm, s, A, lda, B, M, N, K, C, ldc);                            \
+#define QMOE_GR(RR, KC)                                                                            \
+  case KC:                                                                                         \
+    hipLaunchKernelGGL((gemv_reg_kernel<MT, RR, KC, MODE>), dim3(unsigned((N + 4 * RR - 1) / (4 * RR))), \
+                       dim3(256), shm, s, A, lda, B, M, N, K, C, ldc);                             \
     return hip_status("qmoe_gemm(gemv)");
-    QMOE_GR(4, 1)
-    QMOE_GR(4, 2)
-    QMOE_GR(4, 4)
-    QMOE_GR(2, 8)
+    QMOE_GR(R, 1)
+    QMOE_GR(R, 2)
+    QMOE_GR(R, 4)
+    QMOE_GR((R > 2 ? 2 : R), 8)
 #undef QMOE_GR
     default:
       return fail(QMOE_ERR_INVALID, "qmoe_gemm: gemv register path needs K in {512, 1024, 2048, 4096}");
