@@ -119,16 +119,18 @@ def time_graph(fn, steps_per_replay, steps, warmup):
     return secs, ev0.elapsed_time(ev1) * 1e-3, reps * steps_per_replay
 
 
-def event_time_experts(run_one, n, sleep_cycles=60_000_000):
-    """Average GPU duration of run_one(i) bracketed by HIP events on the
-    current stream.  A spin kernel is queued first so every launch is already
-    enqueued when the GPU reaches it (the events then time GPU work only)."""
+def event_time_experts(run_one, n):
+    """Average and median GPU duration of run_one(i), each call bracketed by
+    HIP events on the current stream, in steady state: n untimed calls first
+    (clocks and memory state settle under the same load), then n timed ones
+    enqueued back to back (each call takes hundreds of microseconds, so the
+    host stays ahead and the GPU never idles between them)."""
     import torch
 
+    for i in range(n):
+        run_one(i)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    torch.cuda.synchronize()
-    torch.cuda._sleep(sleep_cycles)
     for i in range(n):
         starts[i].record()
         run_one(i)
@@ -224,6 +226,61 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "top_expert_share": float(cnt.max() / cnt.sum()),
     }
+
+
+def measure_peaks(dev):
+    """Measured ceilings next to the published ones: the bf16 MFMA rate of a
+    pure v_mfma_f32_32x32x16_bf16 loop (probe library) on random and on
+    constant operands (the chip is power-limited: random data lowers the
+    clock), and a plain device-to-device copy of 1 GiB (STREAM-like)."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "nki-moe-7013_amd", "qmoe", "libqmoe_probe.so")
+    lib = ctypes.CDLL(path)
+    lib.qmoe_probe_mfma.restype = ctypes.c_int
+    lib.qmoe_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.qmoe_probe_mfma_flops.restype = ctypes.c_double
+    lib.qmoe_probe_mfma_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks, iters = 2 * n_cu, 2048
+    g = torch.Generator(device=dev).manual_seed(11)
+    rnd = torch.randn(blocks * 8 * 256 * 8, generator=g, device=dev).to(torch.bfloat16)
+    const = torch.ones_like(rnd)
+    out = torch.empty(blocks * 256, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for name, src in (("random", rnd), ("constant", const)):
+        def launch():
+            rc = lib.qmoe_probe_mfma(ctypes.c_void_p(src.data_ptr()), blocks, iters,
+                                     ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream))
+            if rc:
+                raise RuntimeError(f"qmoe_probe_mfma failed ({rc})")
+        launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        secs = e0.elapsed_time(e1) * 1e-3 / 5
+        res[f"mfma_bf16_{name}_TFLOPs"] = round(lib.qmoe_probe_mfma_flops(blocks, iters) / secs / 1e12, 1)
+    del rnd, const, out
+    a = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    res["hbm_copy_GBps"] = round(2 * a.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    return res
 
 
 def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
@@ -490,6 +547,12 @@ def main():
         extra["model_48L"] = model_child()
         print(f"[bench] model: {extra['model_48L']}", file=sys.stderr, flush=True)
 
+    peaks = measure_peaks(dev)
+    print(f"[bench] measured peaks: {peaks}", file=sys.stderr, flush=True)
+    if "prefill_T4096" in extra:
+        extra["prefill_T4096"]["experts_frac_of_measured_mfma"] = (
+            extra["prefill_T4096"]["experts_TFLOPs"] / peaks["mfma_bf16_random_TFLOPs"])
+
     cpu = None
     if not a.no_cpu_baseline:
         cpu = cpu_baseline(layers[0], a.cpu_seconds, dev)
@@ -524,6 +587,8 @@ def main():
                                            if "prefill_T4096" in extra else None),
         "prefill_experts_mfma_frac": (round(extra["prefill_T4096"]["experts_mfma_frac"], 4)
                                       if "prefill_T4096" in extra else None),
+        "prefill_experts_frac_of_measured_mfma": (
+            round(extra["prefill_T4096"]["experts_frac_of_measured_mfma"], 4) if "prefill_T4096" in extra else None),
         "model_decode_tokens_per_s": (round(extra["model_48L"]["decode_tokens_per_s"], 2)
                                       if "decode_tokens_per_s" in extra.get("model_48L", {}) else None),
         "model_decode_hbm_frac": (round(extra["model_48L"]["decode_GBps"] / HBM_PEAK_GBS, 4)
@@ -547,7 +612,9 @@ def main():
                                 for k, v in traffic.items()} if traffic else None),
             "algorithmic_bytes_per_launch": dec["block_bytes"],
             "launch_us_mean": round(dec["us_per_block"], 3),
+            "frac_of_measured_copy": round(achieved / peaks["hbm_copy_GBps"], 4),
         },
+        "measured_peaks": peaks,
         "cpu_baseline": cpu,
         "extra": extra or None,
         "git": git_sha(),

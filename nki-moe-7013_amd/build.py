@@ -3,8 +3,10 @@
     python nki-moe-7013_amd/build.py [-j N]
 
 Each csrc/*.hip / *.cpp is compiled by hipcc into _build/*.o (in parallel),
-then linked into qmoe/libqmoe.so next to the Python bindings.  Every HIP
-translation unit is built with packed-FP32 instruction selection disabled.
+then linked into qmoe/libqmoe.so next to the Python bindings; probes/*.hip
+(measurement kernels that bench.py uses for measured peaks, not part of the
+C ABI) go into qmoe/libqmoe_probe.so.  Every HIP translation unit is built
+with packed-FP32 instruction selection disabled.
 """
 
 from __future__ import annotations
@@ -21,6 +23,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "qmoe", "libqmoe.so")
+PROBES = os.path.join(PKG, "probes")
+PROBE_LIB = os.path.join(PKG, "qmoe", "libqmoe_probe.so")
 ARCH = "gfx950"
 
 COMMON = [
@@ -69,6 +73,14 @@ def build(jobs: int = 8) -> str:
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
+    # measurement probes (bench.py's measured peaks): a library of their own
+    psrcs = sorted(os.path.join(PROBES, f) for f in os.listdir(PROBES) if f.endswith(".hip"))
+    pobjs = [_compile(p) for p in psrcs]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", PROBE_LIB + ".tmp", *pobjs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("probe link failed:\n" + r.stdout + r.stderr)
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     return LIB
 
 
