@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--no-model", action="store_true",
                     help="skip the full 48-layer model (TTFT at 640 tokens, 256 greedy steps; "
                          "run in a child process)")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="only the T=4096 prefill MoE block (Zipf-skewed routing); prints its dict")
     ap.add_argument("--only-model", action="store_true",
                     help="time only the full model, in this process, and print its numbers as JSON")
     return ap.parse_args()
@@ -508,7 +510,7 @@ def main():
         traffic_probe(a.tokens)
         return
     traffic = None
-    if not a.no_traffic and not a.only_model and a.tokens <= 8:  # before this process touches the GPU
+    if not a.no_traffic and not a.only_model and not a.only_prefill and a.tokens <= 8:  # before this process touches the GPU
         traffic = measure_traffic(a.tokens)
         print(f"[bench] traffic: {traffic}", file=sys.stderr, flush=True)
     import torch
@@ -523,6 +525,13 @@ def main():
         print(f"[bench] model: {res}", file=sys.stderr, flush=True)
         print(json.dumps({"workload": "Qwen3-30B-A3B-shaped model, 48 layers, random-init bf16, batch 1, "
                                       "640-token prompt, 256 greedy steps", **res}))
+        return
+    if a.only_prefill:
+        layers = make_layers(min(a.layers, 4), dev)
+        res = bench_prefill(layers, dev)
+        print(f"[bench] prefill: {res}", file=sys.stderr, flush=True)
+        print(json.dumps({"workload": "Qwen3-30B-A3B MoE block, prefill T=4096, Zipf(1.1)-skewed routing, "
+                                      "4 rotating layers", **res}))
         return
     t_setup = time.perf_counter()
     layers = make_layers(a.layers, dev)
