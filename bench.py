@@ -362,6 +362,19 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     torch.cuda.synchronize()
     ttft_ms = ev[0].elapsed_time(ev[1])
     dec_ms = ev[1].elapsed_time(ev[2])
+    # prompt-lookup speculation (spec_len 5) on the same prompt: the same tokens,
+    # several verified per step when the n-gram candidates agree
+    spec_out, _ = m.spec_generate(prompt, 8, spec_len=5)  # warm-up: captures the verify graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    spec_out, spec_stats = m.spec_generate(prompt, new_tokens + 1, spec_len=5)
+    torch.cuda.synchronize()
+    spec_ms = (time.perf_counter() - t0) * 1e3 - ttft_ms
+    # leading tokens identical to plain greedy: the verification pass (5-token
+    # shapes) and the one-token step round differently, so the two paths may
+    # part at a near-tied step (top-2 logits within ~1e-3 on this random model)
+    same = (spec_out[0, prompt_len + 1:].cpu() == toks[0].cpu()).int()
+    spec_prefix = int(same.cumprod(0).sum())
     params_b = 61.06e9  # bytes of bf16 weights (30.53 B params)
     return {
         "ttft_ms": ttft_ms,
@@ -371,6 +384,10 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
         "decode_bytes_per_token_GB": 6.083,
         "decode_GBps": 6.083e9 / (dec_ms / new_tokens * 1e-3) / 1e9,
         "distinct_tokens": int(torch.unique(toks).numel()),
+        "spec_decode_tokens_per_s": new_tokens / (spec_ms * 1e-3),
+        "spec_tokens_per_verify": (spec_stats["accepted"] + spec_stats["verify_steps"]) / max(1, spec_stats["verify_steps"]),
+        "spec_steps": spec_stats["steps"],
+        "spec_greedy_prefix_match": spec_prefix,
     }
 
 
@@ -606,6 +623,8 @@ def main():
                           if "ttft_ms" in extra.get("model_48L", {}) else None),
         "model_prefill_tokens_per_s": (round(extra["model_48L"]["prefill_tokens_per_s"], 1)
                                        if "prefill_tokens_per_s" in extra.get("model_48L", {}) else None),
+        "model_spec_decode_tokens_per_s": (round(extra["model_48L"]["spec_decode_tokens_per_s"], 1)
+                                           if "spec_decode_tokens_per_s" in extra.get("model_48L", {}) else None),
         "roofline": {
             "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
                        "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else

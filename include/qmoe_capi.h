@@ -241,6 +241,17 @@ int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_b
                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                       int64_t start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
 
+/* qmoe_attn_prefill with the chunk start in device memory (start: i32 [1],
+ * read by the kernel and clamped into [0, S_max - S]), so that one captured
+ * launch serves every position: the multi-token verification step of
+ * prompt-lookup speculative decoding (S = spec_len query tokens at
+ * start..start+S-1 against the cache).
+ * Replaces: the speculation model's verification pass over the candidate
+ *   tokens (`_spec_generate`, qwen_with_nki.py:575-1211; spec_len 5, line 74). */
+int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                         int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
+                         const int32_t* start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
+
 /* Decode attention (split-KV flash decoding on MFMA: one partial per 64
  * cache entries, then a merge), one query per batch row that sees cache
  * entries [0, ctx_len[b]).

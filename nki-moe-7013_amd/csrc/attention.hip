@@ -166,10 +166,14 @@ __device__ __forceinline__ int vt_slot(int key) {
   return s * 16 + h * 8 + jj;
 }
 
+// start_dev, when not null, holds the chunk start in device memory (read here,
+// clamped into [0, S_max - S]) so a captured graph can replay the same
+// launch at a new position; otherwise `start` is used.
 __global__ __launch_bounds__(256) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int S, int Hq, int Hkv, int S_max, int start,
-    float scale_log2, uint16_t* __restrict__ out) {
+    const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out) {
+  if (start_dev) start = min(max(start_dev[0], 0), S_max - S);
   __shared__ __attribute__((aligned(16))) uint16_t Ks[AP_KT * AP_LDK];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * AP_LDV];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -573,8 +577,23 @@ extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   dim3 grid(unsigned((S + AP_QT - 1) / AP_QT), unsigned(Hq), unsigned(B));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
-                     int(S), int(Hq), int(Hkv), int(S_max), int(start), scale_log2, out);
+                     int(S), int(Hq), int(Hkv), int(S_max), int(start), nullptr, scale_log2, out);
   return hip_status("qmoe_attn_prefill");
+}
+
+extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                                    int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
+                                    const int32_t* start, float scale, qmoe_bf16* out, qmoe_stream_t stream) {
+  QMOE_REQUIRE(q && k_cache && v_cache && start && out, "qmoe_attn_prefill_at: null pointer");
+  QMOE_REQUIRE(D == HD, "qmoe_attn_prefill_at: head_dim must be 128");
+  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill_at: bad heads");
+  QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max, "qmoe_attn_prefill_at: need S <= S_max");
+  if (B == 0 || S == 0) return QMOE_OK;
+  dim3 grid(unsigned((S + AP_QT - 1) / AP_QT), unsigned(Hq), unsigned(B));
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
+                     int(S), int(Hq), int(Hkv), int(S_max), 0, start, scale_log2, out);
+  return hip_status("qmoe_attn_prefill_at");
 }
 
 extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t S_max) {

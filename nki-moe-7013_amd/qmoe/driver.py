@@ -2,9 +2,10 @@
 
 ``prepare_inference`` mirrors main.py:372-433 (config objects -> model ->
 compile -> load -> tokenizer -> generation config) and ``run_generation``
-mirrors main.py:634-649, on the MI355X model class.  Only greedy decoding is
-implemented.  With no local checkpoint the model is random-init (seeded) and
-prompts are token ids.
+mirrors main.py:634-649, on the MI355X model class.  Decoding is greedy,
+optionally with prompt-lookup speculation (``--speculation-length 5``: the
+reference's shipped setting).  With no local checkpoint the model is
+random-init (seeded) and prompts are token ids.
 
     python -m qmoe.driver --model-path random --prompt-ids 1,2,3 --seq-len 64
 """
@@ -42,6 +43,8 @@ def parse_args(argv=None):
     p.add_argument("--enable-nki", action="store_true", help="accepted for main.py compatibility")
     p.add_argument("--skip-compile", action="store_true")
     p.add_argument("--do-sample", action="store_true")
+    p.add_argument("--speculation-length", type=int, default=0,
+                   help="prompt-lookup speculation: tokens verified per step (the reference ships 5); 0 = off")
     return p.parse_args(argv)
 
 
@@ -51,7 +54,8 @@ def prepare_inference(model_cls, args):
     neuron_config = model_cls.get_neuron_config_cls()(
         batch_size=kw.get("batch_size", 1), seq_len=kw.get("seq_len", 640),
         max_length=kw.get("seq_len", 640), torch_dtype=kw.get("torch_dtype", "bfloat16"),
-        tp_degree=kw.get("tp_degree", 1), seed=kw.get("seed", 0))
+        tp_degree=kw.get("tp_degree", 1), seed=kw.get("seed", 0),
+        speculation_length=kw.get("speculation_length", 0))
     path = args.model_path
     load_config = None
     if path and os.path.isfile(os.path.join(path, "config.json")):

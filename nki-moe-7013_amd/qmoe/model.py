@@ -61,6 +61,9 @@ class MoENeuronConfig:
             raise ValueError("this build runs on one GPU: tp_degree must be 1")
         self.on_device_sampling_config = kwargs.pop("on_device_sampling_config", None)
         self.enable_fused_speculation = False
+        # prompt-lookup speculation: candidates + 1 tokens verified per step
+        # (the reference ships 5, qwen_with_nki.py:74); 0 or 1 = plain greedy
+        self.speculation_length = int(kwargs.pop("speculation_length", 0))
         self.use_hip_graphs = bool(kwargs.pop("use_hip_graphs", True))
         self.seed = int(kwargs.pop("seed", 0))
         self.extra = kwargs  # every other generate-mode flag, accepted and ignored
@@ -449,6 +452,102 @@ class NeuronQwen3MoeForCausalLM:
         self._graphs[B] = st
         return st
 
+    # -- prompt-lookup speculative decoding ---------------------------------------
+    def spec_generate(self, prompt: torch.Tensor, max_new_tokens: int, spec_len: int = 5,
+                      ngram: int = 4, ngram_min: int = 1, strategy: str = "majority1"):
+        """Greedy generation with prompt-lookup speculation (batch 1): each
+        step proposes up to ``spec_len - 1`` tokens from n-gram matches in the
+        tokens so far, verifies ``[last, candidates]`` in one ``spec_len``-token
+        pass (a captured graph) and keeps the candidates that agree with the
+        model's greedy choice plus the model's next token; with no match it
+        runs the one-token decode step.  Restates ``_spec_generate``
+        (qwen_with_nki.py:575-1211) without its adaptive gating and tracing.
+        Returns (tokens ``[1, T0 + max_new_tokens]``, stats dict)."""
+        from . import speculative
+
+        if prompt.dim() != 2 or prompt.shape[0] != 1:
+            raise ValueError("spec_generate takes one prompt [1, T0]")
+        if spec_len < 2:
+            raise ValueError("spec_len must be at least 2")
+        T0 = prompt.shape[1]
+        cap = self.model.layers[0].cache.capacity
+        if T0 + max_new_tokens > cap:
+            raise ValueError(f"prompt + new tokens ({T0}+{max_new_tokens}) exceed the cache ({cap})")
+        self.reset()
+        seq = prompt[0].tolist()
+        if max_new_tokens <= 0:
+            return prompt.clone(), {"steps": 0, "verify_steps": 0, "accepted": 0}
+        first = int(self.prefill(prompt).argmax(-1)[0])
+        seq.append(first)
+        stats = {"steps": 0, "verify_steps": 0, "accepted": 0}
+        k = spec_len - 1
+        while len(seq) - T0 < max_new_tokens:
+            last = seq[-1]
+            cand, _ = speculative.prompt_lookup(seq, k, ngram, ngram_min, strategy)
+            room = max_new_tokens - (len(seq) - T0)
+            cand = cand[: max(0, room - 1)]
+            stats["steps"] += 1
+            if cand and self.position + spec_len <= cap:
+                st = self._verify_graph(spec_len)
+                toks = [last] + speculative.pad_candidates(cand, k)
+                st["tok"].copy_(torch.tensor(toks, dtype=torch.long))
+                st["pos"].copy_(torch.arange(self.position, self.position + spec_len, dtype=torch.int32))
+                st["start"].fill_(self.position)
+                st["graph"].replay()
+                target = st["out"].tolist()
+                m, emitted = speculative.accept(cand, target)
+                stats["verify_steps"] += 1
+                stats["accepted"] += m
+                self.position += m + 1  # cache rows of last and the accepted candidates are final
+                seq.extend(emitted)
+            else:
+                nxt = self.greedy_decode(torch.tensor([last], device=self.device), 1)
+                seq.append(int(nxt[0, 0]))
+        self.model.check_embed()
+        out = torch.tensor(seq[: T0 + max_new_tokens], dtype=torch.long).view(1, -1)
+        return out, stats
+
+    def _verify_graph(self, S: int):
+        """Captured ``S``-token pass at a device-resident position (batch 1):
+        embedding, 48 layers (attention over the cache with the chunk start read
+        on the device), final norm + lm_head for all S rows, per-row argmax."""
+        key = ("verify", S)
+        st = self._graphs.get(key)
+        if st is not None:
+            return st
+        dev, m = self.device, self.model
+        st = {"tok": torch.zeros(S, dtype=torch.long, device=dev),
+              "pos": torch.zeros(S, dtype=torch.int32, device=dev),
+              "start": torch.zeros(1, dtype=torch.int32, device=dev),
+              "h": torch.empty(S, self.config.hidden_size, device=dev),
+              "logits": torch.empty(S, self.config.vocab_size, device=dev),
+              "out": torch.zeros(S, dtype=torch.long, device=dev),
+              "am_ws": ops.argmax_workspace(S, dev)}
+
+        def step():
+            h = m.hidden(st["tok"].view(1, S), st["pos"], 1, S, st["start"], h_buf=st["h"])
+            m.logits(h, out=st["logits"])
+            ops.argmax(st["logits"], out=st["out"], workspace=st["am_ws"])
+
+        # warm-up and capture write cache rows [position, position + S): rows the
+        # first real verification at this position overwrites
+        st["pos"].copy_(torch.arange(self.position, self.position + S, dtype=torch.int32))
+        st["start"].fill_(self.position)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
+        st["graph"] = g
+        self._graphs[key] = st
+        return st
+
+
 
 def _to_device(params, device):
     if isinstance(params, torch.Tensor):
@@ -482,6 +581,10 @@ class HuggingFaceGenerationAdapter:
         if S + max_new_tokens > m.neuron_config.max_length + 1:
             raise ValueError(f"prompt + new tokens ({S}+{max_new_tokens}) exceed max_length "
                              f"{m.neuron_config.max_length}")
+        spec = int(getattr(m.neuron_config, "speculation_length", 0))
+        if spec >= 2 and B == 1 and max_new_tokens > 1:
+            out, _ = m.spec_generate(input_ids, max_new_tokens, spec_len=spec)
+            return out.to(m.device)
         m.reset()
         logits = m.prefill(input_ids)
         first = logits.argmax(dim=-1)

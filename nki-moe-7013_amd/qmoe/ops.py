@@ -441,9 +441,12 @@ def qkv_norm_rope_workspace(T: int, H: int, Hq: int, Hkv: int, D: int) -> int:
 
 
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, B: int, S: int,
-                 start: int = 0, scale: Optional[float] = None,
+                 start=0, scale: Optional[float] = None,
                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Causal GQA attention of ``q[B*S, Hq, D]`` against the cache; returns ``[B*S, Hq*D]``."""
+    """Causal GQA attention of ``q[B*S, Hq, D]`` against the cache; returns ``[B*S, Hq*D]``.
+    ``start`` (cache index of the first query) is an int, or an int32 ``[1]``
+    device tensor read by the kernel (clamped into ``[0, S_max - S]``), so a
+    captured graph replays the call at any position."""
     T, Hq, D = q.shape
     if T != B * S:
         raise ValueError("q must be [B*S, Hq, D]")
@@ -456,6 +459,15 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     out = torch.empty(T, Hq * D, dtype=BF16, device=q.device) if out is None else out
     _need(out, "out", BF16, (T, Hq * D))
+    if isinstance(start, torch.Tensor):
+        _need(start, "start", I32, (1,))
+        _same_device(q, k_cache, v_cache, out, start)
+        check(
+            lib().qmoe_attn_prefill_at(_ptr(q), _ptr(k_cache), _ptr(v_cache), B, S, Hq, Hkv, D, S_max,
+                                       _ptr(start), float(scale), _ptr(out), _stream()),
+            "qmoe_attn_prefill_at",
+        )
+        return out
     _same_device(q, k_cache, v_cache, out)
     check(
         lib().qmoe_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), B, S, Hq, Hkv, D, S_max,

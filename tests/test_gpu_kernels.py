@@ -383,6 +383,38 @@ def test_attn_prefill(dev, B, S, start):
                        max_abs_tol=2e-2, mean_rel_tol=5e-3)
 
 
+@pytest.mark.parametrize("B,S,start", [(1, 5, 0), (1, 5, 613), (2, 8, 130)])
+def test_attn_prefill_device_start(dev, B, S, start):
+    """The chunk start read from device memory (qmoe_attn_prefill_at) gives
+    the same bits as the host-argument form, including replays of one
+    captured launch at two positions."""
+    announce(f"attn_prefill_at B={B} S={S} start={start}")
+    S_max = start + S + 40
+    g = torch.Generator(device=dev).manual_seed(S + start)
+    q = bf16_randn((B * S, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    ref = ops.attn_prefill(q, kc, vc, B, S, start)
+    st = torch.tensor([start], dtype=torch.int32, device=dev)
+    got = ops.attn_prefill(q, kc, vc, B, S, st)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    out = torch.empty_like(ref)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.attn_prefill(q, kc, vc, B, S, st, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.attn_prefill(q, kc, vc, B, S, st, out=out)
+    for p in (start + 17, start):
+        st.fill_(p)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ops.attn_prefill(q, kc, vc, B, S, p))
+
+
 @pytest.mark.parametrize("ctx", [[1], [300, 1000, 17], [8192] * 2])
 def test_attn_decode(dev, ctx):
     announce(f"attn_decode ctx={ctx}")
