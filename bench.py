@@ -317,14 +317,16 @@ def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
         pd = torch.full((B,), L - 1, device=dev, dtype=torch.int32)
         cl = pd + 1
 
-        def dec():
-            att.forward(xd, rd, pd, B, 1, cache, cos, sin, 0, cl)
-
-        secs, ev_secs, done = time_graph(dec, 1, 200, 20)
-        us = ev_secs / done * 1e6
         byts = ((Hq + 2 * Hkv) * D * Hd + Hd * Hq * D) * 2 + B * Hkv * L * D * 2 * 2
-        out[f"decode_ctx{L}_us"] = us
-        out[f"decode_ctx{L}_GBps"] = byts / (us * 1e-6) / 1e9
+        bucket = min(cap, 1 << max(8, (L - 1).bit_length()))  # the model's decode-graph bucket
+        for tag, mc in (("", bucket), ("_full_launch", None)):
+            def dec():
+                att.forward(xd, rd, pd, B, 1, cache, cos, sin, 0, cl, max_ctx=mc)
+
+            secs, ev_secs, done = time_graph(dec, 1, 200, 20)
+            us = ev_secs / done * 1e6
+            out[f"decode_ctx{L}{tag}_us"] = us
+            out[f"decode_ctx{L}{tag}_GBps"] = byts / (us * 1e-6) / 1e9
     return out
 
 

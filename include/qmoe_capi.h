@@ -241,6 +241,19 @@ int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_b
                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                       int64_t start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
 
+/* qmoe_attn_decode for contexts known to fit a bucket: ctx_len[b] <= max_ctx
+ * <= S_max (larger values are clamped to max_ctx).  The launch is sized for
+ * max_ctx instead of the cache capacity S_max (the row stride), so a decode
+ * graph captured per context bucket launches no workgroups for cache rows no
+ * query can see; partial needs qmoe_attn_decode_workspace(B, Hq, D, max_ctx)
+ * floats.
+ * Replaces: the per-bucket token-generation graphs of NxDI (main.py:156-161;
+ *   qwen_with_nki.py:10892-10916) for the attention step. */
+int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                            const int32_t* ctx_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                            int64_t S_max, int64_t max_ctx, float scale, float* partial, qmoe_bf16* out,
+                            qmoe_stream_t stream);
+
 /* qmoe_attn_prefill with the chunk start in device memory (start: i32 [1],
  * read by the kernel and clamped into [0, S_max - S]), so that one captured
  * launch serves every position: the multi-token verification step of

@@ -49,13 +49,15 @@ class Attention:
         self._ws = {}
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
-                cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start: int = 0,
-                ctx_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+                cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start=0,
+                ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
         """``x[B*S, H]`` bf16 (input-normed), ``residual[B*S, H]`` f32 (updated
         in place), ``positions[B*S]`` i32 (RoPE position == cache index).
 
-        S > 1: causal prefill of a chunk starting at cache index ``start``.
-        S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1).
+        S > 1: causal prefill of a chunk starting at cache index ``start`` (an
+        int, or an int32 ``[1]`` device tensor for graph replays at any position).
+        S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1),
+        at most ``max_ctx`` when a context bucket is given.
         """
         qws = self._ws.get(("qkv", B * S))
         if qws is None:
@@ -73,6 +75,7 @@ class Attention:
             if ws is None:
                 ws = ops.attn_decode_workspace(B, self.n_q, self.head_dim, cache.capacity, x.device)
                 self._ws[(B, cache.capacity)] = ws
-            o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale, ws)
+            o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale, ws,
+                                max_ctx=max_ctx)
         ops.gemm(o, self.wo, _lib.GEMM_ADD_F32, out=residual)
         return residual

@@ -146,12 +146,12 @@ class NeuronQwen3MoeDecoderLayer:
         self.mlp = MoEBlock(w["router"], w["w13"], w["w2"], c.num_experts_per_tok)
         self.cache: Optional[KVCache] = None
 
-    def run(self, h: torch.Tensor, positions: torch.Tensor, B: int, S: int, rope, start: int = 0,
-            ctx_len: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def run(self, h: torch.Tensor, positions: torch.Tensor, B: int, S: int, rope, start=0,
+            ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
         """In-place layer on the fp32 residual ``h[B*S, H]``."""
         eps = self.input_layernorm.eps
         x = ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
-        self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len)
+        self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx)
         self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
         return h
 
@@ -193,12 +193,13 @@ class NeuronQwen3MoeModel:
         for l in self.layers:
             l.cache = KVCache(B, c.num_key_value_heads, S_max, c.head_dim, self.embed_tokens.device)
 
-    def hidden(self, input_ids: torch.Tensor, positions: torch.Tensor, B: int, S: int, start: int,
-               ctx_len: Optional[torch.Tensor] = None, h_buf: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def hidden(self, input_ids: torch.Tensor, positions: torch.Tensor, B: int, S: int, start,
+               ctx_len: Optional[torch.Tensor] = None, h_buf: Optional[torch.Tensor] = None,
+               max_ctx: Optional[int] = None) -> torch.Tensor:
         """fp32 final hidden states ``[B*S, H]`` (before the final norm)."""
         h = ops.embed(input_ids.reshape(-1).long(), self.embed_tokens, out=h_buf, err=self.embed_err)
         for layer in self.layers:
-            layer.run(h, positions, B, S, self.rope, start, ctx_len)
+            layer.run(h, positions, B, S, self.rope, start, ctx_len, max_ctx)
         return h
 
     def check_embed(self) -> None:
@@ -399,42 +400,62 @@ class NeuronQwen3MoeForCausalLM:
                 toks.append(cur)
             self.model.check_embed()
             return torch.stack(toks, dim=1)
-        st = self._decode_graph(B)
+        st = self._decode_state(B)
         st["tok"].copy_(first_token.to(self.device).view(B).long())
         st["pos"].fill_(self.position)
         out = torch.empty(B, n_steps, dtype=torch.long, device=self.device)
         for i in range(n_steps):
-            st["graph"].replay()
+            self._decode_graph(B, self._bucket(self.position + i + 1)).replay()
             out[:, i].copy_(st["tok"])
         self.position += n_steps
         self.model.check_embed()
         return out
 
-    def _decode_graph(self, B: int):
-        st = self._graphs.get(B)
-        if st is not None:
-            return st
-        dev, m = self.device, self.model
-        st = {"tok": torch.zeros(B, dtype=torch.long, device=dev),
-              "pos": torch.zeros(B, dtype=torch.int32, device=dev),
-              "h": torch.empty(B, self.config.hidden_size, device=dev),
-              "logits": torch.empty(B, self.config.vocab_size, device=dev),
-              "am_ws": ops.argmax_workspace(B, dev)}
+    # Decode graphs, one per (batch, context bucket): the attention launch of a
+    # bucket covers cache rows [0, bucket) only.  Buckets double from 256 up to
+    # the cache capacity.
+    DECODE_BUCKET_MIN = 256
+
+    def _bucket(self, ctx: int) -> int:
+        cap = self.model.layers[0].cache.capacity
+        b = self.DECODE_BUCKET_MIN
+        while b < ctx and b < cap:
+            b *= 2
+        return min(b, cap)
+
+    def _decode_state(self, B: int):
+        """Step buffers shared by every bucket's graph of batch ``B``."""
+        st = self._graphs.get(("state", B))
+        if st is None:
+            dev = self.device
+            st = {"tok": torch.zeros(B, dtype=torch.long, device=dev),
+                  "pos": torch.zeros(B, dtype=torch.int32, device=dev),
+                  "h": torch.empty(B, self.config.hidden_size, device=dev),
+                  "logits": torch.empty(B, self.config.vocab_size, device=dev),
+                  "am_ws": ops.argmax_workspace(B, dev)}
+            self._graphs[("state", B)] = st
+        return st
+
+    def _decode_graph(self, B: int, bucket: int):
+        key = ("decode", B, bucket)
+        g = self._graphs.get(key)
+        if g is not None:
+            return g
+        m, st = self.model, self._decode_state(B)
 
         # Every op of the step is a library kernel or an elementwise torch op:
         # no reduction that records a memset into the graph (torch's argmax
         # over a 151,936-wide row would), so replays stay correct.
         def step():
             ctx = st["pos"] + 1
-            h = m.hidden(st["tok"].view(B, 1), st["pos"], B, 1, 0, ctx_len=ctx, h_buf=st["h"])
+            h = m.hidden(st["tok"].view(B, 1), st["pos"], B, 1, 0, ctx_len=ctx, h_buf=st["h"], max_ctx=bucket)
             m.logits(h, out=st["logits"])
             ops.argmax(st["logits"], out=st["tok"], workspace=st["am_ws"])
             st["pos"].add_(1)
 
         # Warm-up on a side stream (allocations, lazily created workspaces), then
-        # capture.  The warm-up writes one K/V cache slot: use the slot the next
-        # real step overwrites anyway (the current position).
-        st["pos"].fill_(self.position)
+        # capture.  The warm-up writes one K/V cache slot: the slot at the
+        # current step position, which the next real step overwrites.
         saved = (st["tok"].clone(), st["pos"].clone())
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -448,9 +469,8 @@ class NeuronQwen3MoeForCausalLM:
         st["tok"].copy_(saved[0])
         st["pos"].copy_(saved[1])
         torch.cuda.synchronize()
-        st["graph"] = g
-        self._graphs[B] = st
-        return st
+        self._graphs[key] = g
+        return g
 
     # -- prompt-lookup speculative decoding ---------------------------------------
     def spec_generate(self, prompt: torch.Tensor, max_new_tokens: int, spec_len: int = 5,

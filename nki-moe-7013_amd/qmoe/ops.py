@@ -484,9 +484,10 @@ def attn_decode_workspace(B: int, Hq: int, D: int, S_max: int, device) -> torch.
 
 def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, ctx_len: torch.Tensor,
                 scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
     """One query per batch row (``q[B, Hq, D]``) over cache entries ``[0, ctx_len[b])``;
-    returns ``[B, Hq*D]``."""
+    returns ``[B, Hq*D]``.  ``max_ctx`` (a context bucket, ``ctx_len <= max_ctx
+    <= S_max``) sizes the launch for the bucket instead of the cache capacity."""
     B, Hq, D = q.shape
     _need(q, "q", BF16)
     _need(k_cache, "k_cache", BF16)
@@ -504,6 +505,14 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, c
     out = torch.empty(B, Hq * D, dtype=BF16, device=q.device) if out is None else out
     _need(out, "out", BF16, (B, Hq * D))
     _same_device(q, k_cache, v_cache, ctx_len, workspace, out)
+    if max_ctx is not None and max_ctx < S_max:
+        check(
+            lib().qmoe_attn_decode_bucket(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ctx_len), B, Hq, Hkv, D,
+                                          S_max, int(max_ctx), float(scale), _ptr(workspace), _ptr(out),
+                                          _stream()),
+            "qmoe_attn_decode_bucket",
+        )
+        return out
     check(
         lib().qmoe_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ctx_len), B, Hq, Hkv, D,
                                S_max, float(scale), _ptr(workspace), _ptr(out), _stream()),

@@ -383,6 +383,24 @@ def test_attn_prefill(dev, B, S, start):
                        max_abs_tol=2e-2, mean_rel_tol=5e-3)
 
 
+@pytest.mark.parametrize("ctx,bucket", [([1], 256), ([300, 1000, 17], 1024), ([256], 256)])
+def test_attn_decode_bucket(dev, ctx, bucket):
+    """A launch sized for a context bucket gives the same bits as the one sized
+    for the whole cache (S_max 2048): the live splits and the merge are the
+    same work."""
+    announce(f"attn_decode_bucket ctx={ctx} bucket={bucket}")
+    B, S_max = len(ctx), 2048
+    g = torch.Generator(device=dev).manual_seed(sum(ctx) + bucket)
+    q = bf16_randn((B, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    cl = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    ref = ops.attn_decode(q, kc, vc, cl)
+    got = ops.attn_decode(q, kc, vc, cl, max_ctx=bucket)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("B,S,start", [(1, 5, 0), (1, 5, 613), (2, 8, 130)])
 def test_attn_prefill_device_start(dev, B, S, start):
     """The chunk start read from device memory (qmoe_attn_prefill_at) gives

@@ -160,3 +160,19 @@ def test_spec_generate_matches_greedy(dev, n_layers, n_new):
     assert spec.shape == greedy.shape
     assert stats["verify_steps"] > 0 and stats["accepted"] > 0
     assert torch.equal(spec, greedy)
+
+
+def test_decode_graphs_across_context_buckets(dev):
+    """Greedy decoding that crosses the 256-row context bucket (a new graph
+    with a larger attention launch mid-sequence) matches eager decoding."""
+    announce("decode graphs across buckets, 2 layers")
+    cfg = _config(2, 300)
+    m = qn.NeuronQwen3MoeForCausalLM(None, cfg)
+    m.load()
+    prompt = torch.randint(0, cfg.vocab_size, (1, 248), generator=torch.Generator().manual_seed(4))
+    out_graph = qn.HuggingFaceGenerationAdapter(m).generate(prompt, max_new_tokens=24)
+    m.neuron_config.use_hip_graphs = False
+    out_eager = qn.HuggingFaceGenerationAdapter(m).generate(prompt, max_new_tokens=24)
+    torch.cuda.synchronize()
+    assert ("decode", 1, 256) in m._graphs and ("decode", 1, 301) in m._graphs
+    assert torch.equal(out_graph.cpu(), out_eager.cpu())
