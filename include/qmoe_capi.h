@@ -204,6 +204,17 @@ int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slo
 int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
               int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream);
 
+/* One-row GEMV with the input RMSNorm fused into its activation staging:
+ *   C[n] (mode as qmoe_gemm) = bf16(rms_w * h * rsqrt(mean(h^2) + eps)) . B[n]^T
+ *   h: f32 [K] (the residual stream row); rms_w: bf16 [K]; B: bf16 [N, K].
+ *   The normalised row has the same bits as qmoe_rmsnorm_residual's output,
+ *   so C matches qmoe_rmsnorm_residual followed by qmoe_gemm, in one launch.
+ *   Limits: K in {512, 1024, 2048, 4096}.
+ * Replaces: input_layernorm feeding the attention's QKV projection in the
+ *   decoder layer (qwen_with_nki.py:10155-10213, NKIRMSNorm 1286-1415). */
+int qmoe_gemv_rmsnorm(const float* h, const qmoe_bf16* rms_w, float eps, const qmoe_bf16* B, int64_t N,
+                      int64_t K, int mode, void* C, qmoe_stream_t stream);
+
 /* QKV projection with per-head RMSNorm over head_dim and RoPE fused into the
  * epilogue; K/V written straight into the contiguous cache.
  *   x: bf16 [B*S, H]; wqkv: bf16 [(Hq+2*Hkv)*D, H] (q rows, then k, then v);
@@ -223,6 +234,20 @@ int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv, const qmoe_bf1
                        int64_t H, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
                        qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache, float* workspace,
                        qmoe_stream_t stream);
+
+/* The second half of qmoe_qkv_norm_rope's decode path on its own, for callers
+ * that produce the raw projection another way (qmoe_gemv_rmsnorm with the
+ * input RMSNorm fused in): per (token, head) RMSNorm over head_dim and RoPE
+ * for q and k, q to q_out, k / v rows into the cache at positions[t].
+ *   qkv: f32 [B*S, (Hq + 2*Hkv)*D] before normalisation; other arguments as
+ *   qmoe_qkv_norm_rope.  Limits: D == 128, B*S <= 16.
+ * Replaces: q_layernorm/k_layernorm, RoPE and the KV-cache update of
+ *   NeuronQwen3MoEAttention (qwen_with_nki.py:10102-10103, 10083-10087,
+ *   9943-9946). */
+int qmoe_qkv_finish(const float* qkv, const qmoe_bf16* q_norm_w, const qmoe_bf16* k_norm_w,
+                    const float* rope_cos, const float* rope_sin, int64_t max_pos, const int32_t* positions,
+                    int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
+                    qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache, qmoe_stream_t stream);
 
 /* Workspace bytes of qmoe_qkv_norm_rope for T = B*S token rows: T * (Hq +
  * 2*Hkv) * D * 4 when T <= 16 and H in {512, 1024, 2048, 4096} with T*H <=

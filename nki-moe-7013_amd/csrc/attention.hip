@@ -564,6 +564,26 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
   return hip_status("qmoe_qkv_norm_rope");
 }
 
+extern "C" int qmoe_qkv_finish(const float* qkv, const qmoe_bf16* q_norm_w, const qmoe_bf16* k_norm_w,
+                               const float* rope_cos, const float* rope_sin, int64_t max_pos,
+                               const int32_t* positions, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                               int64_t D, int64_t S_max, float eps, qmoe_bf16* q_out, qmoe_bf16* k_cache,
+                               qmoe_bf16* v_cache, qmoe_stream_t stream) {
+  QMOE_REQUIRE(qkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && q_out && k_cache && v_cache,
+               "qmoe_qkv_finish: null pointer");
+  QMOE_REQUIRE(D == HD, "qmoe_qkv_finish: head_dim must be 128 (D=%lld)", (long long)D);
+  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq + 2 * Hkv < 65536, "qmoe_qkv_finish: bad head counts");
+  QMOE_REQUIRE(B >= 0 && S >= 0 && B * S <= QKV_DEC_MAX_T, "qmoe_qkv_finish: need B*S <= 16");
+  QMOE_REQUIRE(S_max > 0 && max_pos > 0, "qmoe_qkv_finish: bad S_max/max_pos");
+  const int64_t T = B * S;
+  if (T == 0) return QMOE_OK;
+  const int max_p = int(std::min<int64_t>(max_pos, 1ll << 30));
+  hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv)), dim3(64), 0, as_stream(stream), qkv,
+                     q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(T), int(S), int(Hq), int(Hkv),
+                     int(S_max), max_p, eps, q_out, k_cache, v_cache);
+  return hip_status("qmoe_qkv_finish");
+}
+
 extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
                                  const qmoe_bf16* v_cache, int64_t B, int64_t S, int64_t Hq,
                                  int64_t Hkv, int64_t D, int64_t S_max, int64_t start, float scale,

@@ -129,6 +129,67 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(const uint16_t* __restric
   }
 }
 
+// Single-row GEMV with the input RMSNorm fused into the activation staging:
+// x = bf16(w_rms * h * rsqrt(mean(h^2) + eps)) from the fp32 residual row h,
+// with the same chunking, summation order and rounding as
+// rmsnorm_residual_kernel (so x has the same bits), then the one-row-per-wave
+// dot of gemv_reg_kernel.  Weight loads are issued first, so the norm's
+// reduction overlaps the weight stream.
+template <int KC, int MODE>
+__global__ __launch_bounds__(256) void gemv_rms_kernel(const float* __restrict__ h,
+                                                       const uint16_t* __restrict__ rms_w, float eps,
+                                                       const uint16_t* __restrict__ B, int N,
+                                                       void* __restrict__ C) {
+  constexpr int K = KC * 512, NCH = K / 4 / 256 > 0 ? K / 4 / 256 : 1;  // float4 chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t xs[K];
+  __shared__ float red[4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int n0 = blockIdx.x * 4 + wave;
+  u32x4 w[KC];
+  {
+    const uint16_t* brow = B + int64_t(min(n0, N - 1)) * K + lane * 8;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) w[c] = ld_stream(brow + c * 512);
+  }
+  float4 v[NCH];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = t + j * 256;
+    if (c < K / 4) {
+      const float4 a = reinterpret_cast<const float4*>(h)[c];
+      v[j] = a;
+      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tot += red[i];
+  const float r = rsqrtf(tot / float(K) + eps);
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = t + j * 256;
+    if (c < K / 4) {
+      const float4 a = v[j];
+      const uint2 wv = reinterpret_cast<const uint2*>(rms_w)[c];
+      uint2 o;
+      o.x = pack_bf16x2(bf16_lo(wv.x) * (a.x * r), bf16_hi(wv.x) * (a.y * r));
+      o.y = pack_bf16x2(bf16_lo(wv.y) * (a.z * r), bf16_hi(wv.y) * (a.w * r));
+      reinterpret_cast<uint2*>(xs)[c] = o;
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < KC; ++c)
+    acc = dot8_bf16(w[c], *reinterpret_cast<const u32x4*>(xs + c * 512 + lane * 8), acc);
+  const float out = wave_sum(acc);
+  if (lane == 0 && n0 < N) store_out<MODE>(C, n0, out);
+}
+
 // Skinny GEMM for 2 <= M <= 16 rows of A (batched decode), K = 128 * KS:
 // v_mfma_f32_16x16x32_bf16 with the A rows padded to 16 (zeros past M).  A
 // workgroup owns NB (8 or 16) output columns; wave w owns the K range
@@ -404,6 +465,49 @@ int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, in
 }
 
 }  // namespace qmoe
+
+namespace qmoe {
+template <int MODE>
+static int launch_gemv_rms(const float* h, const uint16_t* rms_w, float eps, const uint16_t* B, int N, int K,
+                           void* C, hipStream_t s) {
+  const dim3 grid(unsigned((N + 3) / 4));
+  switch (K / 512) {
+#define QMOE_GRMS(KC)                                                                                \
+  case KC:                                                                                           \
+    hipLaunchKernelGGL((gemv_rms_kernel<KC, MODE>), grid, dim3(256), 0, s, h, rms_w, eps, B, N, C); \
+    return hip_status("qmoe_gemv_rmsnorm");
+    QMOE_GRMS(1)
+    QMOE_GRMS(2)
+    QMOE_GRMS(4)
+    QMOE_GRMS(8)
+#undef QMOE_GRMS
+    default:
+      return fail(QMOE_ERR_INVALID, "qmoe_gemv_rmsnorm: K must be 512, 1024, 2048 or 4096");
+  }
+}
+
+int gemv_rmsnorm_launch(const float* h, const uint16_t* rms_w, float eps, const uint16_t* B, int64_t N,
+                        int64_t K, int mode, void* C, hipStream_t s) {
+  QMOE_REQUIRE(h && rms_w && B && C, "qmoe_gemv_rmsnorm: null pointer");
+  QMOE_REQUIRE(N > 0 && N < (1ll << 31), "qmoe_gemv_rmsnorm: bad N");
+  QMOE_REQUIRE(K == 512 || K == 1024 || K == 2048 || K == 4096, "qmoe_gemv_rmsnorm: K must be 512, 1024, 2048 or 4096");
+  QMOE_REQUIRE(mode >= 0 && mode <= 2, "qmoe_gemv_rmsnorm: bad mode %d", mode);
+  QMOE_REQUIRE(eps >= 0.0f, "qmoe_gemv_rmsnorm: eps < 0");
+  switch (mode) {
+    case QMOE_GEMM_STORE_BF16:
+      return launch_gemv_rms<QMOE_GEMM_STORE_BF16>(h, rms_w, eps, B, int(N), int(K), C, s);
+    case QMOE_GEMM_STORE_F32:
+      return launch_gemv_rms<QMOE_GEMM_STORE_F32>(h, rms_w, eps, B, int(N), int(K), C, s);
+    default:
+      return launch_gemv_rms<QMOE_GEMM_ADD_F32>(h, rms_w, eps, B, int(N), int(K), C, s);
+  }
+}
+}  // namespace qmoe
+
+extern "C" int qmoe_gemv_rmsnorm(const float* h, const qmoe_bf16* rms_w, float eps, const qmoe_bf16* B,
+                                 int64_t N, int64_t K, int mode, void* C, qmoe_stream_t stream) {
+  return qmoe::gemv_rmsnorm_launch(h, rms_w, eps, B, N, K, mode, C, qmoe::as_stream(stream));
+}
 
 extern "C" int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
                          int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream) {

@@ -6,6 +6,9 @@ namespace qmoe {
 // C = A . B^T (see qmoe_gemm in qmoe_capi.h).
 int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N,
                 int64_t K, int mode, void* C, int64_t ldc, hipStream_t s);
+// C[N] = bf16(rmsnorm(h)) . B^T for one fp32 row h (see qmoe_gemv_rmsnorm).
+int gemv_rmsnorm_launch(const float* h, const uint16_t* rms_w, float eps, const uint16_t* B, int64_t N,
+                        int64_t K, int mode, void* C, hipStream_t s);
 }  // namespace qmoe
 
 namespace qmoe {

@@ -50,7 +50,8 @@ class Attention:
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
                 cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start=0,
-                ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
+                ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None,
+                norm: Optional[tuple] = None) -> torch.Tensor:
         """``x[B*S, H]`` bf16 (input-normed), ``residual[B*S, H]`` f32 (updated
         in place), ``positions[B*S]`` i32 (RoPE position == cache index).
 
@@ -58,14 +59,24 @@ class Attention:
         int, or an int32 ``[1]`` device tensor for graph replays at any position).
         S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1),
         at most ``max_ctx`` when a context bucket is given.
+        ``norm = (rms_w, eps)``: ``x`` is the fp32 residual row itself (B*S == 1)
+        and the input RMSNorm is fused into the QKV GEMV.
         """
+        n_ws = ops.qkv_norm_rope_workspace(B * S, x.shape[1], self.n_q, self.n_kv, self.head_dim)
         qws = self._ws.get(("qkv", B * S))
         if qws is None:
-            n = ops.qkv_norm_rope_workspace(B * S, x.shape[1], self.n_q, self.n_kv, self.head_dim)
-            qws = torch.empty(max(n // 4, 1), dtype=torch.float32, device=x.device)
+            qws = torch.empty(max(n_ws // 4, 1), dtype=torch.float32, device=x.device)
             self._ws[("qkv", B * S)] = qws
-        q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
-                              self.n_q, self.n_kv, cache.k, cache.v, self.eps, workspace=qws)
+        if norm is not None:
+            if B * S != 1 or n_ws == 0:
+                raise ValueError("the fused input norm takes one fp32 row on the GEMV path")
+            raw = qws[: n_ws // 4].view(1, -1)
+            ops.gemv_rmsnorm(x, norm[0], norm[1], self.wqkv, _lib.GEMM_STORE_F32, out=raw)
+            q = ops.qkv_finish(raw, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S, self.n_q,
+                               self.n_kv, cache.k, cache.v, self.eps)
+        else:
+            q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
+                                  self.n_q, self.n_kv, cache.k, cache.v, self.eps, workspace=qws)
         if S > 1:
             o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
         else:

@@ -150,8 +150,14 @@ class NeuronQwen3MoeDecoderLayer:
             ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
         """In-place layer on the fp32 residual ``h[B*S, H]``."""
         eps = self.input_layernorm.eps
-        x = ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
-        self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx)
+        if B * S == 1 and ops.qkv_norm_rope_workspace(1, h.shape[1], self.self_attn.n_q, self.self_attn.n_kv,
+                                                      self.self_attn.head_dim) > 0:
+            # one-token step: the input RMSNorm runs inside the QKV GEMV's staging
+            self.self_attn.forward(h, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx,
+                                   norm=(self.input_layernorm.weight, eps))
+        else:
+            x = ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
+            self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx)
         self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
         return h
 

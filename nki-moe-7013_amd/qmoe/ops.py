@@ -386,6 +386,58 @@ def gemm(A: torch.Tensor, B: torch.Tensor, mode: int = _lib.GEMM_STORE_BF16,
     return out
 
 
+def gemv_rmsnorm(h: torch.Tensor, rms_w: torch.Tensor, eps: float, B: torch.Tensor,
+                 mode: int = _lib.GEMM_STORE_BF16, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``bf16(rmsnorm(h[1,K])) . B[N,K]^T`` in one launch (the same bits as
+    :func:`rmsnorm_residual` then :func:`gemm`)."""
+    if h.dim() != 2 or h.shape[0] != 1 or B.dim() != 2 or h.shape[1] != B.shape[1]:
+        raise ValueError("h must be [1,K] and B [N,K]")
+    K, N = h.shape[1], B.shape[0]
+    _need(h, "h", F32)
+    _need(rms_w, "rms_w", BF16, (K,))
+    _need(B, "B", BF16)
+    if out is None:
+        if mode == _lib.GEMM_ADD_F32:
+            raise ValueError("mode ADD_F32 needs out")
+        out = torch.empty(1, N, dtype=BF16 if mode == _lib.GEMM_STORE_BF16 else F32, device=h.device)
+    _need(out, "out", BF16 if mode == _lib.GEMM_STORE_BF16 else F32, (1, N))
+    _same_device(h, rms_w, B, out)
+    check(lib().qmoe_gemv_rmsnorm(_ptr(h), _ptr(rms_w), float(eps), _ptr(B), N, K, int(mode), _ptr(out), _stream()),
+          "qmoe_gemv_rmsnorm")
+    return out
+
+
+def qkv_finish(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+               rope_cos: torch.Tensor, rope_sin: torch.Tensor, positions: torch.Tensor, B: int, S: int,
+               Hq: int, Hkv: int, k_cache: torch.Tensor, v_cache: torch.Tensor, eps: float,
+               q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-head q/k RMSNorm + RoPE from the raw projection ``qkv[B*S, (Hq+2Hkv)*D]``
+    (f32), K/V rows into the cache; returns ``q[B*S, Hq, D]`` (bf16)."""
+    T = B * S
+    D = q_norm_w.shape[0]
+    _need(qkv, "qkv", F32, (T, (Hq + 2 * Hkv) * D))
+    _need(q_norm_w, "q_norm_w", BF16, (D,))
+    _need(k_norm_w, "k_norm_w", BF16, (D,))
+    max_pos = rope_cos.shape[0]
+    _need(rope_cos, "rope_cos", F32, (max_pos, D // 2))
+    _need(rope_sin, "rope_sin", F32, (max_pos, D // 2))
+    _need(positions, "positions", I32, (T,))
+    if k_cache.dim() != 4 or k_cache.shape[:2] != (B, Hkv) or k_cache.shape[3] != D:
+        raise ValueError(f"k_cache must be [B={B}, Hkv={Hkv}, S_max, D={D}]")
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    q_out = torch.empty(T, Hq, D, dtype=BF16, device=qkv.device) if q_out is None else q_out
+    _need(q_out, "q_out", BF16, (T, Hq, D))
+    _same_device(qkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, k_cache, v_cache, q_out)
+    check(
+        lib().qmoe_qkv_finish(_ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cos), _ptr(rope_sin), max_pos,
+                              _ptr(positions), B, S, Hq, Hkv, D, k_cache.shape[2], float(eps), _ptr(q_out),
+                              _ptr(k_cache), _ptr(v_cache), _stream()),
+        "qmoe_qkv_finish",
+    )
+    return q_out
+
+
 # ----------------------------------------------------------------- attention
 def qkv_norm_rope(
     x: torch.Tensor, wqkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,

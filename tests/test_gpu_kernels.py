@@ -383,6 +383,48 @@ def test_attn_prefill(dev, B, S, start):
                        max_abs_tol=2e-2, mean_rel_tol=5e-3)
 
 
+@pytest.mark.parametrize("K,N", [(512, 100), (2048, 5120), (4096, 2048)])
+def test_gemv_rmsnorm_fused(dev, K, N):
+    """The input RMSNorm fused into the one-row GEMV gives the same bits as
+    qmoe_rmsnorm_residual followed by qmoe_gemm, in every epilogue mode; and
+    gemv_rmsnorm + qkv_finish equals qkv_norm_rope on the normed row."""
+    announce(f"gemv_rmsnorm K={K} N={N}")
+    g = torch.Generator(device=dev).manual_seed(K + N)
+    h = torch.randn(1, K, generator=g, device=dev) * 3.0
+    w = (1.0 + 0.2 * torch.randn(K, generator=g, device=dev)).to(torch.bfloat16)
+    B = bf16_randn((N, K), g, dev, std=0.02)
+    x = ops.rmsnorm_residual(h, w, 1e-6)
+    for mode in (_lib.GEMM_STORE_BF16, _lib.GEMM_STORE_F32):
+        ref = ops.gemm(x, B, mode)
+        got = ops.gemv_rmsnorm(h, w, 1e-6, B, mode)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"mode {mode}"
+    acc_ref = torch.randn(1, N, generator=g, device=dev)
+    acc_got = acc_ref.clone()
+    ops.gemm(x, B, _lib.GEMM_ADD_F32, out=acc_ref)
+    ops.gemv_rmsnorm(h, w, 1e-6, B, _lib.GEMM_ADD_F32, out=acc_got)
+    torch.cuda.synchronize()
+    assert torch.equal(acc_got, acc_ref)
+
+
+def test_qkv_finish_matches_qkv_norm_rope(dev, attn_w):
+    announce("qkv_finish vs qkv_norm_rope, one token")
+    wqkv, qn, kn = attn_w
+    g = torch.Generator(device=dev).manual_seed(21)
+    h = torch.randn(1, H, generator=g, device=dev)
+    w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    pos = torch.tensor([37], dtype=torch.int32, device=dev)
+    cos, sin = _rope(64, dev)
+    kc1 = torch.zeros(1, HKV, 64, D, dtype=torch.bfloat16, device=dev)
+    vc1, kc2, vc2 = torch.zeros_like(kc1), torch.zeros_like(kc1), torch.zeros_like(kc1)
+    q1 = ops.qkv_norm_rope(ops.rmsnorm_residual(h, w, 1e-6), wqkv, qn, kn, cos, sin, pos, 1, 1, HQ, HKV, kc1, vc1,
+                           1e-6)
+    raw = ops.gemv_rmsnorm(h, w, 1e-6, wqkv, _lib.GEMM_STORE_F32)
+    q2 = ops.qkv_finish(raw, qn, kn, cos, sin, pos, 1, 1, HQ, HKV, kc2, vc2, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
 @pytest.mark.parametrize("ctx,bucket", [([1], 256), ([300, 1000, 17], 1024), ([256], 256)])
 def test_attn_decode_bucket(dev, ctx, bucket):
     """A launch sized for a context bucket gives the same bits as the one sized
