@@ -92,7 +92,10 @@ int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float*
  *   tile_m rows; meta: i32 [4] = (n_tiles, n_active, error, -): error is 1
  *   when an id is outside [0, E) (then n_tiles = n_active = 0 and the slot
  *   maps are the identity); meta[3] is not touched.
- *   max_tiles must be >= ceil(T*k / tile_m) + E.
+ *   max_tiles = rows of `tiles`, at least ceil(T*k / tile_m) + E.  With
+ *   max_tiles >= qmoe_moe_permute_tiles(T, k, E, tile_m) and T*k > 4096 the
+ *   work is spread over one workgroup per 1024 pairs, using the rows past
+ *   ceil(T*k / tile_m) + E as scratch; otherwise one workgroup does it all.
  * Replaces: the block metadata ExpertMLPsV2 builds for
  *   torch_blockwise_matmul_inference (token_position_to_id / block_to_expert,
  *   qwen_with_nki.py:5872-5881, 5478-5479; dedup 5656-5667 made unnecessary). */
@@ -100,6 +103,12 @@ int qmoe_moe_permute(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E,
                      int64_t tile_m, int64_t max_tiles, int32_t* counts, int32_t* offsets,
                      int32_t* slot_token, int32_t* token_slot, int32_t* active,
                      int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
+
+/* Rows of `tiles` for which qmoe_moe_permute / qmoe_moe_route spread the
+ * placement over several workgroups: ceil(T*k / tile_m) + E + ceil(C*(E+1)/4)
+ * with C = ceil(T*k / 1024) chunks (-1 for a non-positive k, E or tile_m).
+ * Replaces: nothing in the reference (a sizing helper of this library). */
+int64_t qmoe_moe_permute_tiles(int64_t T, int64_t k, int64_t E, int64_t tile_m);
 
 /* Routing in one call: router logits + top-k (as qmoe_router_topk) followed by
  * the dispatch metadata (as qmoe_moe_permute), same argument meanings.

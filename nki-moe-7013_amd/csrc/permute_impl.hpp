@@ -142,46 +142,44 @@ __device__ void permute_block(const int32_t* idx, int N, int k, int E, int tile_
   }
 }
 
-// rank_out[s] for pairs s in [c0, c0 + n): run[e] on entry plus the number of
-// earlier pairs of the range routed to the same expert (stable: increasing s);
-// run[e] ends up advanced by the range's count of expert e.  Same wave-ballot
-// / cross-wave prefix scheme as permute_block.  Every thread must call it.
+// One round of NT consecutive pairs, thread t holding pair t's expert e
+// (valid = the pair exists; e in [0, E) when valid): returns run[e] on entry
+// plus the number of earlier pairs of the round routed to the same expert
+// (stable: increasing pair index); run[e] ends up advanced by the round's
+// count of expert e.  Same wave-ballot / cross-wave prefix scheme as
+// permute_block.  Every thread must call it.
 template <int NT>
-__device__ void rank_range(const int32_t* idx, int c0, int n, int32_t* rank_out, int* run,
-                           int (&wave_cnt)[NT / 64][PERM_MAX_E], int E) {
+__device__ int rank_round(int e, bool valid, int* run, int (&wave_cnt)[NT / 64][PERM_MAX_E], int E) {
   constexpr int WAVES = NT / 64;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int b0 = 0; b0 < n; b0 += NT) {
-    const int s = c0 + b0 + t;
-    const bool valid = b0 + t < n;
-    const int e = valid ? idx[s] : 0;
-    unsigned long long match = __ballot(valid);
+  if (!valid) e = 0;
+  unsigned long long match = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const unsigned long long bal = __ballot((e >> b) & 1);
-      match &= ((e >> b) & 1) ? bal : ~bal;
-    }
-    const int rank = __popcll(match & lt_mask);
-    const int cnt = __popcll(match);
-    for (int i = t; i < WAVES * PERM_MAX_E; i += NT) (&wave_cnt[0][0])[i] = 0;
-    __syncthreads();
-    if (valid && rank == 0) wave_cnt[wave][e] = cnt;
-    __syncthreads();
-    if (t < E) {
-      int r = run[t];
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const int m = wave_cnt[w][t];
-        wave_cnt[w][t] = r;
-        r += m;
-      }
-      run[t] = r;
-    }
-    __syncthreads();
-    if (valid) rank_out[s] = wave_cnt[wave][e] + rank;
-    __syncthreads();
+  for (int b = 0; b < 8; ++b) {
+    const unsigned long long bal = __ballot((e >> b) & 1);
+    match &= ((e >> b) & 1) ? bal : ~bal;
   }
+  const int rank = __popcll(match & lt_mask);
+  const int cnt = __popcll(match);
+  for (int i = t; i < WAVES * PERM_MAX_E; i += NT) (&wave_cnt[0][0])[i] = 0;
+  __syncthreads();
+  if (valid && rank == 0) wave_cnt[wave][e] = cnt;
+  __syncthreads();
+  if (t < E) {
+    int r = run[t];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const int m = wave_cnt[w][t];
+      wave_cnt[w][t] = r;
+      r += m;
+    }
+    run[t] = r;
+  }
+  __syncthreads();
+  const int out = valid ? wave_cnt[wave][e] + rank : 0;
+  __syncthreads();
+  return out;
 }
 
 }  // namespace qmoe

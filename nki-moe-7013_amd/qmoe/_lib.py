@@ -34,6 +34,7 @@ PROTOTYPES = {
     "qmoe_rmsnorm_residual": (c_int, [P, P, P, I64, I64, c_float, P, P, P]),
     "qmoe_router_topk": (c_int, [P, P, P, I64, I64, I64, I64, P, P, P, P]),
     "qmoe_moe_permute": (c_int, [P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
+    "qmoe_moe_permute_tiles": (I64, [I64, I64, I64, I64]),
     "qmoe_moe_route": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P]),
     "qmoe_moe_decode_block": (
         c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, P, P, P]),

@@ -129,18 +129,19 @@ class Route:
     slot_token: torch.Tensor  # [T*k]
     token_slot: torch.Tensor  # [T*k]
     active: torch.Tensor  # [E]
-    tiles: torch.Tensor  # [max_tiles, 4]
-    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, arrival counter)
+    tiles: torch.Tensor  # [rows >= max_tiles, 4]: the tile table, then permutation scratch
+    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, unused)
     logits: Optional[torch.Tensor] = None  # [T, E] f32 (filled by moe_route)
     topk_idx: Optional[torch.Tensor] = None  # [T, k] i32
     topk_w: Optional[torch.Tensor] = None  # [T, k] f32
 
     @staticmethod
     def alloc(T: int, k: int, E: int, tile_m: int, device, with_topk: bool = False) -> "Route":
-        max_tiles = -(-T * k // tile_m) + E
+        max_tiles = -(-T * k // tile_m) + E  # bound on the number of tiles
+        rows = int(lib().qmoe_moe_permute_tiles(T, k, E, tile_m))
         z = lambda *s: torch.empty(*s, dtype=I32, device=device)
         r = Route(T, k, E, tile_m, max_tiles, z(E), z(E + 1), z(T * k), z(T * k), z(E),
-                  z(max_tiles, 4), torch.zeros(4, dtype=I32, device=device))
+                  z(max(rows, max_tiles), 4), z(4))
         if with_topk:
             r.logits = torch.empty(T, E, dtype=F32, device=device)
             r.topk_idx = z(T, k)
@@ -157,7 +158,7 @@ def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Option
         raise ValueError("route buffers were allocated for a different shape")
     check(
         lib().qmoe_moe_permute(
-            _ptr(topk_idx), T, k, E, tile_m, route.max_tiles, _ptr(route.counts), _ptr(route.offsets),
+            _ptr(topk_idx), T, k, E, tile_m, route.tiles.shape[0], _ptr(route.counts), _ptr(route.offsets),
             _ptr(route.slot_token), _ptr(route.token_slot), _ptr(route.active), _ptr(route.tiles),
             _ptr(route.meta), _stream(),
         ),
@@ -182,7 +183,7 @@ def moe_route(x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[to
     _same_device(x, w_router, bias, route.meta)
     check(
         lib().qmoe_moe_route(
-            _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, tile_m, route.max_tiles, _ptr(route.logits),
+            _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, tile_m, route.tiles.shape[0], _ptr(route.logits),
             _ptr(route.topk_idx), _ptr(route.topk_w), _ptr(route.counts), _ptr(route.offsets),
             _ptr(route.slot_token), _ptr(route.token_slot), _ptr(route.active), _ptr(route.tiles),
             _ptr(route.meta), _stream(),

@@ -111,6 +111,16 @@ def test_decode_block_workspace_size():
     assert lib.qmoe_moe_decode_block_workspace(-1, 2048) == -1
 
 
+def test_permute_tiles_rows():
+    """Rows of `tiles` for the per-chunk permutation: the tile-table bound
+    ceil(T*k/tile_m) + E, then (E + 1) ints of scratch per 1024-pair chunk."""
+    l = _lib.lib()
+    assert l.qmoe_moe_permute_tiles(4096, 8, 128, 256) == 128 + 128 + (32 * 129 + 3) // 4
+    assert l.qmoe_moe_permute_tiles(513, 8, 128, 128) == 33 + 128 + (5 * 129 + 3) // 4
+    assert l.qmoe_moe_permute_tiles(0, 8, 128, 128) == 128
+    assert l.qmoe_moe_permute_tiles(4, 8, 128, 0) == -1
+
+
 def test_blocked_down_layout():
     """w2[e, b, h, j] = down[e, 8b + j, h] (NxDI (E, I, H)) = W2[e, h, 8b + j];
     both conversions invert, and the HF path lands on the same bytes."""
