@@ -89,10 +89,15 @@ def make_layers(n_layers, dev, seed=0):
     return layers
 
 
-def time_graph(fn, steps_per_replay, steps, warmup):
+def time_graph(fn, steps_per_replay, steps, warmup, spread=None):
     """Capture fn() (which performs steps_per_replay steps) in a HIP graph and
     time ceil(steps / steps_per_replay) replays.  Returns (seconds by the host
-    clock, seconds by HIP events on the replay stream, steps_done)."""
+    clock, seconds by HIP events on the replay stream, steps_done).
+
+    With ``spread = n``, n further replays (after the timed region, not part
+    of it) are each bracketed by their own HIP events, and the per-step
+    microseconds of every replay are stored in ``spread_us`` (a list passed by
+    the caller) for the median / p10 / p90."""
     import torch
 
     s = torch.cuda.Stream()
@@ -118,7 +123,23 @@ def time_graph(fn, steps_per_replay, steps, warmup):
     ev1.record()
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
+    if spread is not None:
+        n = spread.pop() if spread else 0
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in evs:
+            a.record()
+            graph.replay()
+            b.record()
+        torch.cuda.synchronize()
+        spread.extend(a.elapsed_time(b) * 1e3 / steps_per_replay for a, b in evs)
     return secs, ev0.elapsed_time(ev1) * 1e-3, reps * steps_per_replay
+
+
+def percentiles(us):
+    """median, p10 and p90 (nearest rank) of a list of per-step microseconds."""
+    v = sorted(us)
+    at = lambda q: v[min(len(v) - 1, max(0, int(round(q * (len(v) - 1)))))]
+    return {"median": round(at(0.5), 3), "p10": round(at(0.1), 3), "p90": round(at(0.9), 3), "samples": len(v)}
 
 
 def event_time_experts(run_one, n):
@@ -160,7 +181,8 @@ def bench_decode(layers, T, steps, warmup, dev):
         for l in range(L):
             blocks[l](xs[l], res[l], out=outs[l])
 
-    secs, ev_secs, done = time_graph(all_layers, L, steps, warmup)
+    spread = [60]  # 60 individually timed replays of the L-call graph
+    secs, ev_secs, done = time_graph(all_layers, L, steps, warmup, spread=spread)
     U = []
     for l in range(L):
         _, _, ti = ops.router_topk(xs[l], layers[l][0], K_TOP)
@@ -178,6 +200,7 @@ def bench_decode(layers, T, steps, warmup, dev):
         "block_bytes": block_bytes,
         "block_GBps": block_bytes / (us_per_step * 1e-6) / 1e9,
         "block_frac": block_bytes / (us_per_step * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "us_per_block_spread": percentiles(spread),
         "secs": secs,
         "steps": done,
     }
@@ -201,7 +224,8 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         for l in range(L):
             blocks[l](xs[l])
 
-    secs, ev_secs, done = time_graph(run, L, reps * L, L)
+    spread = [50]
+    secs, ev_secs, done = time_graph(run, L, reps * L, 5 * L, spread=spread)
     counts = []
     for l in range(L):
         _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
@@ -219,10 +243,17 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     mean_ms, med_ms = event_time_experts(run_experts, 4 * L)
     flops = T * K_TOP * 2 * 3 * H * I
     us = ev_secs / done * 1e6
+    # touched experts' weights once, the router, x in and the output, as bf16
+    touched = float((torch.stack(counts) > 0).sum(1).float().mean())
+    block_bytes = touched * EXPERT_BYTES + ROUTER_BYTES + 2 * T * H * 2
     return {
         "T": T,
         "us_per_block": us,
+        "us_per_block_spread": percentiles(spread),
         "tokens_per_s": T / (us * 1e-6),
+        "touched_experts": touched,
+        "block_bytes": block_bytes,
+        "block_hbm_frac": block_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "experts_us_mean": mean_ms * 1e3,
         "experts_TFLOPs": flops / (mean_ms * 1e-3) / 1e12,
         "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
@@ -609,12 +640,15 @@ def main():
         },
         "moe_block_GBps": round(dec["block_GBps"], 1),
         "moe_block_hbm_frac": round(dec["block_frac"], 4),
+        "moe_block_us_spread": dec["us_per_block_spread"],
         # the north-star companions: prefill MoE block (T=4096, Zipf-skewed
         # routing) and the full 48-layer model at batch 1 (child process)
         "prefill_moe_block_tokens_per_s": (round(extra["prefill_T4096"]["tokens_per_s"], 1)
                                            if "prefill_T4096" in extra else None),
         "prefill_experts_mfma_frac": (round(extra["prefill_T4096"]["experts_mfma_frac"], 4)
                                       if "prefill_T4096" in extra else None),
+        "prefill_block_hbm_frac": (round(extra["prefill_T4096"]["block_hbm_frac"], 4)
+                                   if "prefill_T4096" in extra else None),
         "prefill_experts_frac_of_measured_mfma": (
             round(extra["prefill_T4096"]["experts_frac_of_measured_mfma"], 4) if "prefill_T4096" in extra else None),
         "model_decode_tokens_per_s": (round(extra["model_48L"]["decode_tokens_per_s"], 2)

@@ -97,7 +97,7 @@ def router_w(dev):
     return bf16_randn((E, H), g, dev, std=0.02)
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 128, 4096])
+@pytest.mark.parametrize("T", [1, 8, 17, 64, 100, 128, 4096])
 def test_router_topk(dev, router_w, T):
     announce(f"router T={T}")
     g = torch.Generator(device=dev).manual_seed(100 + T)
@@ -125,6 +125,26 @@ def test_router_bias_zipf_selection(dev, router_w):
     assert max_abs(logits, rl) <= 1e-4
     ok = gap_mask(rl, K_TOP)
     assert torch.equal(ti.cpu().long()[ok], ri[ok])
+
+
+# Router at other expert counts, hidden sizes and k: the GEMV path (T <= 16)
+# and the GEMM path (ragged T), with and without a bias.
+@pytest.mark.parametrize("T,E_,H_,k,with_bias", [(12, 64, 512, 4, False), (300, 256, 1024, 8, True),
+                                                 (1000, 128, 4096, 8, True), (77, 128, 192, 8, False)])
+def test_router_topk_shapes(dev, T, E_, H_, k, with_bias):
+    announce(f"router T={T} E={E_} H={H_} k={k} bias={with_bias}")
+    g = torch.Generator(device=dev).manual_seed(7 * T + E_)
+    w = bf16_randn((E_, H_), g, dev, std=0.02)
+    x = bf16_randn((T, H_), g, dev)
+    bias = torch.randn(E_, generator=g, device=dev) * 0.05 if with_bias else None
+    logits, tw, ti = ops.router_topk(x, w, k, bias)
+    torch.cuda.synchronize()
+    rl, rw, ri = oracle.router_topk(x.cpu(), w.cpu(), k, None if bias is None else bias.cpu())
+    assert max_abs(logits, rl) <= 1e-4
+    ok = gap_mask(rl, k)
+    assert ok.float().mean() > 0.5
+    assert torch.equal(ti.cpu().long()[ok], ri[ok])
+    np.testing.assert_allclose(tw.cpu()[ok].numpy(), rw[ok].numpy(), rtol=2e-5, atol=1e-7)
 
 
 # --------------------------------------------------------------------------- permute
