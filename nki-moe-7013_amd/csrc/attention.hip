@@ -94,7 +94,12 @@ __device__ __forceinline__ void qkv_finish_head(
 // Decode-size QKV (T <= QKV_DEC_MAX_T token rows): the projection runs as a
 // bandwidth-bound GEMV over every CU (qmoe_gemm's register GEMV: all weight
 // rows streamed once) into an fp32 workspace [T][(Hq+2Hkv)*D]; this kernel
-// then finishes each (token, head) from there.
+// then finishes each (token, head) from there, one wave per (head, token):
+// lane l holds element l and its RoPE partner l + 64, so the head's values,
+// norm weights and position are all requested at once, the cos/sin row right
+// after the position arrives, and the norm is one wave reduction.  Same
+// arithmetic per element as qkv_finish_head; the sum of squares runs in the
+// wave's reduction order.
 constexpr int QKV_DEC_MAX_T = 16;
 
 __global__ __launch_bounds__(64) void qkv_finish_kernel(
@@ -103,11 +108,31 @@ __global__ __launch_bounds__(64) void qkv_finish_kernel(
     const float* __restrict__ rope_sin, const int32_t* __restrict__ positions, int T, int S, int Hq,
     int Hkv, int S_max, int max_pos, float eps, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
-  const int t = threadIdx.x, head = blockIdx.x;
-  if (t >= 2 * T) return;
-  const int tok = t >> 1;
-  qkv_finish_head(raw + int64_t(tok) * (Hq + 2 * Hkv) * HD + head * HD, t & 1, tok, head, positions, S,
-                  Hq, Hkv, S_max, max_pos, eps, qn_w, kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
+  const int l = threadIdx.x, head = blockIdx.x, tok = blockIdx.y;
+  const float* v = raw + int64_t(tok) * (Hq + 2 * Hkv) * HD + head * HD;
+  const bool normed = head < Hq + Hkv;
+  const uint16_t* nw = head < Hq ? qn_w : kn_w;
+  float lo = v[l], hi = v[l + 64];
+  const float wl = normed ? bf16_to_f32(nw[l]) : 0.0f, wh = normed ? bf16_to_f32(nw[l + 64]) : 0.0f;
+  const int pos = positions[tok];
+  if (pos < 0 || pos >= S_max || pos >= max_pos) return;  // rejected: nothing written
+  const int b = tok / S;
+  uint16_t* dst;
+  if (normed) {
+    const float c = rope_cos[int64_t(pos) * (HD / 2) + l], sn = rope_sin[int64_t(pos) * (HD / 2) + l];
+    const float r = rsqrtf(wave_sum(lo * lo + hi * hi) / float(HD) + eps);
+    const float a = wl * (lo * r), bb = wh * (hi * r);
+    lo = a * c - bb * sn;
+    hi = bb * c + a * sn;
+    if (head < Hq)
+      dst = q_out + (int64_t(tok) * Hq + head) * HD;
+    else
+      dst = k_cache + ((int64_t(b) * Hkv + (head - Hq)) * S_max + pos) * HD;
+  } else {
+    dst = v_cache + ((int64_t(b) * Hkv + (head - Hq - Hkv)) * S_max + pos) * HD;
+  }
+  dst[l] = f32_to_bf16(lo);
+  dst[l + 64] = f32_to_bf16(hi);
 }
 
 __global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
@@ -308,6 +333,7 @@ constexpr int AD_MAX_G = 16;            // q heads per kv head
 constexpr int AD_VT_LD = AD_WKEYS + 8;  // V^T row stride in LDS (bf16): 144 B, 16-byte aligned rows
 constexpr int AD_VCH = AD_WKEYS * HD / 8 / 64;  // 16-byte V chunks per lane (16)
 constexpr int AD_PSTR = HD + 4;         // partial record: m, l, 2 pad, o[HD] (16-byte aligned o)
+constexpr int AD_MERGE_PF = 16;         // o values the merge requests before the max is known
 
 // Completes this wave's LDS writes before its own lanes read them (a wave's
 // DS instructions run in order; this also keeps the compiler from moving
@@ -480,8 +506,18 @@ __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __re
   const int ctx = min(ctx_len[bh / Hq], max_ctx);
   const int live = min(nsub, (ctx + AD_WKEYS - 1) / AD_WKEYS);
   const float* p = partial + int64_t(bh) * nsub * AD_PSTR;
-  float mloc = -INFINITY;
-  for (int s = d; s < live; s += HD) mloc = fmaxf(mloc, p[int64_t(s) * AD_PSTR]);
+  // Loads that do not depend on the running max go out first: this thread's
+  // (m, l) of partial d and the first AD_MERGE_PF o values of its dim.
+  float mv = -INFINITY, lv = 0.0f;
+  if (d < live) {
+    mv = p[int64_t(d) * AD_PSTR];
+    lv = p[int64_t(d) * AD_PSTR + 1];
+  }
+  float ov[AD_MERGE_PF];
+#pragma unroll
+  for (int u = 0; u < AD_MERGE_PF; ++u) ov[u] = u < live ? p[int64_t(u) * AD_PSTR + 4 + d] : 0.0f;
+  float mloc = mv;
+  for (int s = d + HD; s < live; s += HD) mloc = fmaxf(mloc, p[int64_t(s) * AD_PSTR]);
   mloc = wave_max(mloc);
   if (lane == 0) sred[wave] = mloc;
   __syncthreads();
@@ -491,12 +527,20 @@ __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __re
     const int n = min(HD, live - c0);
     __syncthreads();
     if (d < n) {
-      const float m = p[int64_t(c0 + d) * AD_PSTR];
+      const float m = c0 == 0 ? mv : p[int64_t(c0 + d) * AD_PSTR];
+      const float lsum = c0 == 0 ? lv : p[int64_t(c0 + d) * AD_PSTR + 1];
       sw[d] = m == -INFINITY ? 0.0f : __expf(m - M);
-      L += sw[d] * p[int64_t(c0 + d) * AD_PSTR + 1];  // summed over threads below
+      L += sw[d] * lsum;  // summed over threads below
     }
     __syncthreads();
-    for (int s0 = 0; s0 < n; s0 += 8) {
+    int first = 0;
+    if (c0 == 0) {
+#pragma unroll
+      for (int u = 0; u < AD_MERGE_PF; ++u)
+        if (u < n) O = fmaf(sw[u], ov[u], O);
+      first = AD_MERGE_PF;
+    }
+    for (int s0 = first; s0 < n; s0 += 8) {
       float v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) v[u] = s0 + u < n ? p[int64_t(c0 + s0 + u) * AD_PSTR + 4 + d] : 0.0f;
@@ -552,8 +596,8 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
     const int64_t N = (Hq + 2 * Hkv) * HD;
     int rc = gemm_launch(x, H, wqkv, T, N, H, QMOE_GEMM_STORE_F32, workspace, N, as_stream(stream));
     if (rc) return rc;
-    hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv)), dim3(64), 0, as_stream(stream),
-                       workspace, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(T), int(S),
+    hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv), unsigned(T)), dim3(64), 0,
+                       as_stream(stream), workspace, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(T), int(S),
                        int(Hq), int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
     return hip_status("qmoe_qkv_norm_rope(finish)");
   }
@@ -578,7 +622,7 @@ extern "C" int qmoe_qkv_finish(const float* qkv, const qmoe_bf16* q_norm_w, cons
   const int64_t T = B * S;
   if (T == 0) return QMOE_OK;
   const int max_p = int(std::min<int64_t>(max_pos, 1ll << 30));
-  hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv)), dim3(64), 0, as_stream(stream), qkv,
+  hipLaunchKernelGGL(qkv_finish_kernel, dim3(unsigned(Hq + 2 * Hkv), unsigned(T)), dim3(64), 0, as_stream(stream), qkv,
                      q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(T), int(S), int(Hq), int(Hkv),
                      int(S_max), max_p, eps, q_out, k_cache, v_cache);
   return hip_status("qmoe_qkv_finish");

@@ -54,9 +54,12 @@ __global__ __launch_bounds__(64) void block_logits_kernel(
     float eps, const uint16_t* __restrict__ w_router, const float* __restrict__ bias, int T, int H,
     int E, float* __restrict__ logits, uint16_t* __restrict__ x_out) {
   const int lane = threadIdx.x, e = blockIdx.x;
-  u32x4 wr[HC];
+  u32x4 wr[HC], wn[HC];
 #pragma unroll
   for (int c = 0; c < HC; ++c) wr[c] = ld_stream(w_router + int64_t(e) * H + c * 512 + lane * 8);
+#pragma unroll
+  for (int c = 0; c < HC; ++c)  // the norm weights go out with the router row
+    wn[c] = h ? ld16(rms_w + c * 512 + lane * 8) : u32x4{0u, 0u, 0u, 0u};
   const float b = bias ? bias[e] : 0.0f;
   for (int r = 0; r < T; ++r) {
     float xf[HC][8];
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(64) void block_logits_kernel(
 #pragma unroll
       for (int c = 0; c < HC; ++c) {
         float wf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(rms_w + c * 512 + lane * 8), wf);
+        unpack8(wn[c], wf);
         u32x4 o;
         o.x = pack_bf16x2(wf[0] * (xf[c][0] * rr), wf[1] * (xf[c][1] * rr));
         o.y = pack_bf16x2(wf[2] * (xf[c][2] * rr), wf[3] * (xf[c][3] * rr));
@@ -331,6 +334,8 @@ __global__ __launch_bounds__(64 * BLK_RED_WAVES) void block_reduce_kernel(
   const int h = blockIdx.x * 64 + lane, t = blockIdx.y;
   const float* p = partial + int64_t(t) * H + h;
   const int64_t stride = int64_t(T) * H;
+  const int64_t o = int64_t(t) * H + h;
+  const float res = (wave == 0 && residual) ? residual[o] : 0.0f;  // requested with the partials
   float v[PER];
 #pragma unroll
   for (int q = 0; q < PER; ++q) v[q] = p[int64_t(wave + q * BLK_RED_WAVES) * stride];
@@ -343,8 +348,7 @@ __global__ __launch_bounds__(64 * BLK_RED_WAVES) void block_reduce_kernel(
     float v = s_sum[0][lane];
 #pragma unroll
     for (int w = 1; w < BLK_RED_WAVES; ++w) v += s_sum[w][lane];
-    const int64_t o = int64_t(t) * H + h;
-    out[o] = (residual ? residual[o] : 0.0f) + v;
+    out[o] = res + v;
   }
 }
 

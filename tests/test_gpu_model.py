@@ -146,7 +146,11 @@ def _params_of(m):
 def test_spec_generate_matches_greedy(dev, n_layers, n_new):
     """Prompt-lookup speculation (spec_len 5): the verified multi-token steps
     reproduce plain greedy decoding token for token, and on a prompt with
-    repeated n-grams the verification path actually runs and accepts."""
+    repeated n-grams the verification path actually runs and accepts.  The
+    5-token verification computes attention as a causal chunk rather than one
+    decode step per token, so the two paths round differently: they must agree
+    at least up to the first step whose top-2 logit gap (fp32 reference) is
+    below 0.02, as for the greedy-vs-reference comparison."""
     announce(f"spec_generate layers={n_layers} new={n_new}")
     seg = torch.randint(0, 151936, (1, 24), generator=torch.Generator().manual_seed(11))
     prompt = torch.cat([seg, seg, seg[:, :10]], dim=1)  # 58 tokens, repeated 24-grams
@@ -159,7 +163,14 @@ def test_spec_generate_matches_greedy(dev, n_layers, n_new):
     print(f"  spec stats {stats}", flush=True)
     assert spec.shape == greedy.shape
     assert stats["verify_steps"] > 0 and stats["accepted"] > 0
-    assert torch.equal(spec, greedy)
+    if not torch.equal(spec, greedy):
+        P = prompt.shape[1]
+        d = int((spec[0, P:] == greedy[0, P:]).int().cumprod(0).sum())
+        ref = ReferenceModel(_params_of(m), cfg)
+        _, gaps = ref.greedy(prompt.to(dev), n_new)
+        first_tie = next((i for i, gp in enumerate(gaps) if gp < 0.02), n_new)
+        print(f"  spec diverges from greedy at step {d}; first reference near-tie at step {first_tie}", flush=True)
+        assert d >= first_tie
 
 
 def test_decode_graphs_across_context_buckets(dev):
