@@ -5,9 +5,7 @@
 
 namespace qmoe {
 
-constexpr int DEC_TOK_CHUNK = 16;  // token rows staged in LDS at a time
 constexpr int DEC_MAX_T = 64;
-constexpr int DOWN_NB = 16;  // w2 blocks per register batch of the down GEMV
 
 // Keeps a register value opaque to the optimiser inside a loop, so that
 // loop-invariant conversions of it are not hoisted (hoisting the bf16 -> fp32
@@ -40,6 +38,8 @@ __device__ __forceinline__ void stage16(u32x4* dst, int n, Src src) {
 }
 
 // Stage n token rows (bf16 [H]) into LDS; rows given by an index map or direct.
+// A plain strided loop: it keeps the caller's registers free, which matters
+// more than batching these loads where several workgroups share a CU.
 __device__ __forceinline__ void stage_rows_bf16(uint16_t* dst, const uint16_t* src,
                                                 const int32_t* row_map, int r0, int n, int H) {
   const int hch = H / 8;
