@@ -258,6 +258,29 @@ def test_experts_and_combine(dev, experts, T):
                        mean_rel_tol=1e-4 if tight else 5e-3)
 
 
+@pytest.mark.parametrize("T", [20, 64])
+def test_experts_gemv_crowded_experts(dev, experts, T):
+    """The T <= 64 expert GEMVs when a few experts take many tokens: every
+    token routed to experts 0..7 (T rows each, so the gate/up token staging
+    and the 16-row down passes both loop), plus a token order that is not
+    the slot order."""
+    announce(f"experts gemv crowded T={T}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(31 + T)
+    x = bf16_randn((T, H), g, dev)
+    top = torch.stack([torch.randperm(8, generator=torch.Generator().manual_seed(t)) for t in range(T)])
+    top = top.to(torch.int32).to(dev)
+    tw = torch.rand(T, K_TOP, generator=g, device=dev)
+    tw = tw / tw.sum(-1, keepdim=True)
+    route = ops.moe_permute(top, E, 256)
+    y = ops.moe_experts_gemv(x, w13, w2, route)
+    out = ops.moe_combine(y, route, tw)
+    torch.cuda.synchronize()
+    rows = list(range(T))
+    ref = _oracle_rows(x.cpu(), top.cpu(), tw.cpu(), _ExpertCache(w13, w2), rows)
+    assert_close_layer(out.cpu()[rows], ref, f"crowded moe T={T}", max_abs_tol=2e-3, mean_rel_tol=1e-4)
+
+
 @pytest.mark.parametrize("tile_m", [32, 128])
 def test_experts_grouped_small_tiles(dev, experts, tile_m):
     """Grouped experts take any tile table with runs of at most 256 rows: a
