@@ -20,6 +20,7 @@
 //                    per-wave partials that hold keys.
 #include "decode_util.hpp"
 #include "gemm.hpp"
+#include "mfma_pipe.hpp"
 #include "mfma_tile.hpp"
 
 namespace qmoe {
@@ -101,6 +102,10 @@ __device__ __forceinline__ void qkv_finish_head(
 // arithmetic per element as qkv_finish_head; the sum of squares runs in the
 // wave's reduction order.
 constexpr int QKV_DEC_MAX_T = 16;
+#ifndef QMOE_QKV_PIPE_MIN_T
+#define QMOE_QKV_PIPE_MIN_T 2048
+#endif
+constexpr int QKV_PIPE_MIN_T = QMOE_QKV_PIPE_MIN_T;  // token rows from which the 256-row pipeline is used
 
 __global__ __launch_bounds__(64) void qkv_finish_kernel(
     const float* __restrict__ raw, const uint16_t* __restrict__ qn_w,
@@ -178,6 +183,83 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
                   kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
 }
 
+// Large-T QKV: the same per-head epilogue on the direct-to-LDS MFMA pipeline
+// (pipe::Pipe, as qmoe_gemm uses): a workgroup computes BM token rows x one
+// head (128 columns), stages the fp32 accumulators in LDS and finishes the
+// rows with qkv_finish_head, 128 rows per pass.  Workgroups of one row block
+// are consecutive (head fastest), so the x rows they share are read from L2.
+template <class P>
+struct QkvPipe {
+  static constexpr int LDC = HD + 4;
+  static constexpr int EPI = P::BM * LDC * 4;
+  static constexpr int SMEM = P::SMEM > EPI ? P::SMEM : EPI;
+  static_assert(P::BN == HD, "one head per tile");
+  static_assert(SMEM <= 160 * 1024, "LDS");
+};
+
+template <class P>
+__global__ __launch_bounds__(256, 1) void qkv_pipe_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wqkv,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+    const int32_t* __restrict__ positions, int T, int S, int H, int Hq, int Hkv, int S_max,
+    int max_pos, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  constexpr int LDC = QkvPipe<P>::LDC;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int head = blockIdx.x, m0 = blockIdx.y * P::BM, n0 = head * HD;
+  const pipe::i32x4 ra = pipe::make_rsrc(x, uint32_t(int64_t(T) * H * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(wqkv + int64_t(n0) * H, uint32_t(int64_t(HD) * H * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int rr = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(rr, lane);
+    if (j < P::AI)
+      vo[j] = m0 + rr < T ? uint32_t(int64_t(m0 + rr) * H * 2) + c : pipe::PAD;
+    else
+      vo[j] = uint32_t(int64_t(rr) * H * 2) + c;
+  }
+  typename P::Acc acc;
+  P::run(ra, rb, vo, H / P::BK, smem, acc);
+  __syncthreads();  // pipeline buffers are reused for the accumulators
+  float* ct = reinterpret_cast<float*>(smem);  // [BM][LDC] fp32
+#pragma unroll
+  for (int i = 0; i < P::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < P::FN; ++j) {
+      const int col = P::acc_col(wave, j, lane);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ct[P::acc_row(wave, i, e, lane) * LDC + col] = acc[i][j][e];
+    }
+  __syncthreads();
+  for (int r0 = 0; r0 < P::BM; r0 += 128) {
+    const int row = r0 + (t >> 1), tok = m0 + row;
+    if (tok < T)
+      qkv_finish_head(ct + row * LDC, t & 1, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
+                      kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
+  }
+}
+
+template <class P>
+static int qkv_pipe_launch(const uint16_t* x, const uint16_t* wqkv, const uint16_t* qn_w, const uint16_t* kn_w,
+                           const float* rope_cos, const float* rope_sin, const int32_t* positions, int64_t T,
+                           int64_t S, int64_t H, int64_t Hq, int64_t Hkv, int64_t S_max, int max_p, float eps,
+                           uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
+  static const bool attr = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_pipe_kernel<P>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, QkvPipe<P>::SMEM);
+    return true;
+  }();
+  (void)attr;
+  dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + P::BM - 1) / P::BM));
+  hipLaunchKernelGGL(qkv_pipe_kernel<P>, grid, dim3(256), QkvPipe<P>::SMEM, s, x, wqkv, qn_w, kn_w, rope_cos,
+                     rope_sin, positions, int(T), int(S), int(H), int(Hq), int(Hkv), int(S_max), max_p, eps,
+                     q_out, k_cache, v_cache);
+  return hip_status("qmoe_qkv_norm_rope");
+}
+
 // ====================================================================== prefill
 constexpr int AP_QT = 128;      // query rows per workgroup (4 waves x 32)
 constexpr int AP_KT = 64;       // keys per step
@@ -194,7 +276,7 @@ __device__ __forceinline__ int vt_slot(int key) {
 // start_dev, when not null, holds the chunk start in device memory (read here,
 // clamped into [0, S_max - S]) so a captured graph can replay the same
 // launch at a new position; otherwise `start` is used.
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int S, int Hq, int Hkv, int S_max, int start,
     const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out) {
@@ -231,26 +313,57 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   const int kv_end = start + min(q0 + AP_QT, S);  // keys [0, kv_end) can be visible
   const int n_kt = (kv_end + AP_KT - 1) / AP_KT;
 
-  for (int kt = 0; kt < n_kt; ++kt) {
+  // One K/V tile per step, prefetched into registers during the previous
+  // step's MFMAs.  K: chunk c = t + 256 j (key c / 16, dims (c % 16) * 8).
+  // V: item i = t + 256 j: key pair kp = i % 32 (keys 2kp, 2kp + 1, which sit
+  // in adjacent slots of the permuted V^T row) and dim chunk i / 32, so the
+  // transpose into LDS is 32-bit (key pair) writes, the 32 key pairs of a
+  // wave half on distinct banks.
+  u32x4 kreg[4], vreg[2][2];
+  auto gload = [&](int kt) {
     const int kv0 = kt * AP_KT;
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = t + 256 * j;
-      const int key = c >> 4, dc = (c & 15) * 8;
-      const bool ok = kv0 + key < kv_end;
-      const int64_t off = kv_base + int64_t(kv0 + key) * HD + dc;
-      const u32x4 kv = ok ? ld16(k_cache + off) : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 vv = ok ? ld16(v_cache + off) : u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(Ks + key * AP_LDK + dc) = kv;
-      const int vs = vt_slot(key);
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+      const int c = t + 256 * j, key = c >> 4, dc = (c & 15) * 8;
+      kreg[j] = kv0 + key < kv_end ? ld16(k_cache + kv_base + int64_t(kv0 + key) * HD + dc)
+                                   : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        Vt[(dc + 2 * u) * AP_LDV + vs] = uint16_t(w4[u] & 0xffffu);
-        Vt[(dc + 2 * u + 1) * AP_LDV + vs] = uint16_t(w4[u] >> 16);
+    for (int j = 0; j < 2; ++j) {
+      const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int key = 2 * kp + r;
+        vreg[j][r] = kv0 + key < kv_end ? ld16(v_cache + kv_base + int64_t(kv0 + key) * HD + dc)
+                                        : u32x4{0u, 0u, 0u, 0u};
       }
     }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = t + 256 * j, key = c >> 4, dc = (c & 15) * 8;
+      *reinterpret_cast<u32x4*>(Ks + key * AP_LDK + dc) = kreg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
+      const int vs = vt_slot(2 * kp);  // even; key 2kp + 1 is at vs + 1
+      const uint32_t a4[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
+      const uint32_t b4[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        *reinterpret_cast<uint32_t*>(Vt + (dc + 2 * u) * AP_LDV + vs) = (a4[u] & 0xffffu) | (b4[u] << 16);
+        *reinterpret_cast<uint32_t*>(Vt + (dc + 2 * u + 1) * AP_LDV + vs) = (a4[u] >> 16) | (b4[u] & 0xffff0000u);
+      }
+    }
+  };
+  if (n_kt > 0) gload(0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int kv0 = kt * AP_KT;
+    __syncthreads();  // the previous step's LDS reads are done
+    lstore();
+    if (kt + 1 < n_kt) gload(kt + 1);
     __syncthreads();
     // S^T blocks: keys [0,32) and [32,64) x this wave's 32 queries
     f32x16 st[2];
@@ -601,6 +714,10 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                        int(Hq), int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
     return hip_status("qmoe_qkv_norm_rope(finish)");
   }
+  if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32))
+    return qkv_pipe_launch<pipe::Pipe<256, 128, 64, 2>>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                         positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                         k_cache, v_cache, as_stream(stream));
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + tile::BM - 1) / tile::BM));
   hipLaunchKernelGGL(qkv_norm_rope_kernel, grid, dim3(256), 0, as_stream(stream), x, wqkv, q_norm_w,
                      k_norm_w, rope_cos, rope_sin, positions, int(T), int(S), int(H), int(Hq),
