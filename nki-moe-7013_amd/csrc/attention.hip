@@ -103,7 +103,7 @@ __device__ __forceinline__ void qkv_finish_head(
 // wave's reduction order.
 constexpr int QKV_DEC_MAX_T = 16;
 #ifndef QMOE_QKV_PIPE_MIN_T
-#define QMOE_QKV_PIPE_MIN_T 2048
+#define QMOE_QKV_PIPE_MIN_T 256
 #endif
 constexpr int QKV_PIPE_MIN_T = QMOE_QKV_PIPE_MIN_T;  // token rows from which the 256-row pipeline is used
 

@@ -385,10 +385,11 @@ def _rope(max_pos, dev):
     return cos[:, : D // 2].contiguous().to(dev), sin[:, : D // 2].contiguous().to(dev)
 
 
-# B*S <= 16: GEMV + finish path (8, 16: batched decode steps); up to 2047 rows:
-# 128-row MFMA tiles; from 2048 rows: the 256-row pipeline (3 x 900: ragged)
+# B*S <= 16: GEMV + finish path (8, 16: batched decode steps); up to 255 rows:
+# 128-row MFMA tiles; from 256 rows: the 256-row pipeline (3 x 257, 3 x 900:
+# ragged)
 @pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0), (8, 1, 1279), (16, 1, 40),
-                                       (1, 1, 0), (3, 900, 5), (2, 1024, 0)])
+                                       (1, 1, 0), (3, 900, 5), (2, 1024, 0), (1, 200, 3)])
 def test_qkv_norm_rope(dev, attn_w, B, S, start):
     announce(f"qkv_norm_rope B={B} S={S} start={start}")
     wqkv, qn, kn = attn_w
