@@ -288,6 +288,21 @@ int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_cache, const 
                             int64_t S_max, int64_t max_ctx, float scale, float* partial, qmoe_bf16* out,
                             qmoe_stream_t stream);
 
+/* S consecutive queries per batch row, at cache positions start..start+S-1
+ * (start: device int32[1], clamped into [0, S_max - S]); query s attends to
+ * keys [0, start + s].  Computed as B*S single-query problems (the split +
+ * merge of qmoe_attn_decode over the full capacity), which suits the few-token
+ * chunks of speculative verification better than the tiled prefill kernel.
+ *   q: bf16 [B*S][Hq][D]; k_cache, v_cache: [B][Hkv][S_max][D] (the chunk's
+ *   rows already written); partial: qmoe_attn_decode_workspace(B*S, Hq, D,
+ *   S_max) floats; out: bf16 [B*S][Hq*D].  Limits as qmoe_attn_decode, B*S < 65536.
+ * Replaces: the attention of the speculation driver's verification forward
+ *   over the candidate chunk (_spec_generate qwen_with_nki.py:575-1211). */
+int qmoe_attn_decode_chunk(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                           const int32_t* start, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                           int64_t S_max, float scale, float* partial, qmoe_bf16* out,
+                           qmoe_stream_t stream);
+
 /* qmoe_attn_prefill with the chunk start in device memory (start: i32 [1],
  * read by the kernel and clamped into [0, S_max - S]), so that one captured
  * launch serves every position: the multi-token verification step of

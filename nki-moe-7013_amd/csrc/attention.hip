@@ -467,16 +467,28 @@ __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcn
 //       this wave's LDS)
 // Every global load of the wave is issued first (K, V, q), so a split costs
 // one HBM round trip.
+// Query rows: blockIdx.z.  With chunk_start == nullptr each query row is a
+// batch row (cache row = query row) with ctx_len[row] keys; otherwise qpb
+// consecutive query rows share cache row row / qpb and query s = row % qpb
+// sits at position start + s (start = *chunk_start clamped into
+// [0, S_max - qpb]) and sees keys [0, start + s].
+__device__ __forceinline__ int ad_ctx(const int32_t* ctx_len, const int32_t* chunk_start, int row, int qpb,
+                                      int S_max, int max_ctx) {
+  if (chunk_start) return min(max(chunk_start[0], 0), S_max - qpb) + row % qpb + 1;
+  return min(ctx_len[row], max_ctx);
+}
+
 __global__ __launch_bounds__(AD_SUBS * 64) void attn_decode_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
-    const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len, int Hq, int Hkv,
-    int S_max, int max_ctx, int nsub, float scale, float* __restrict__ partial) {
+    const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len,
+    const int32_t* __restrict__ chunk_start, int qpb, int Hq, int Hkv, int S_max, int max_ctx, int nsub,
+    float scale, float* __restrict__ partial) {
   __shared__ __attribute__((aligned(16))) uint16_t vt[AD_SUBS][HD][AD_VT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t pt[AD_SUBS][AD_MAX_G][AD_WKEYS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int kvh = blockIdx.y, b = blockIdx.z, bc = chunk_start ? b / qpb : b;  // query row, cache row
   const int G = Hq / Hkv;
-  const int ctx = min(ctx_len[b], max_ctx);
+  const int ctx = ad_ctx(ctx_len, chunk_start, b, qpb, S_max, max_ctx);
   const int sub = blockIdx.x * AD_SUBS + wave;
   const int kw0 = sub * AD_WKEYS;
   const int nk = min(AD_WKEYS, ctx - kw0);
@@ -491,7 +503,7 @@ __global__ __launch_bounds__(AD_SUBS * 64) void attn_decode_split_kernel(
     }
     return;
   }
-  const int64_t kv_base = (int64_t(b) * Hkv + kvh) * S_max * HD;
+  const int64_t kv_base = (int64_t(bc) * Hkv + kvh) * S_max * HD;
   // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
   u32x4 ka[2][HD / 16];
 #pragma unroll
@@ -610,13 +622,14 @@ __global__ __launch_bounds__(AD_SUBS * 64) void attn_decode_split_kernel(
 // of the chunk, eight loads in flight at a time.
 __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __restrict__ partial,
                                                                const int32_t* __restrict__ ctx_len,
-                                                               int Hq, int max_ctx, int nsub,
+                                                               const int32_t* __restrict__ chunk_start,
+                                                               int qpb, int S_max, int Hq, int max_ctx, int nsub,
                                                                uint16_t* __restrict__ out) {
   __shared__ float sw[HD];
   __shared__ float sred[2];
   const int bh = blockIdx.x;  // b * Hq + h
   const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
-  const int ctx = min(ctx_len[bh / Hq], max_ctx);
+  const int ctx = ad_ctx(ctx_len, chunk_start, bh / Hq, qpb, S_max, max_ctx);
   const int live = min(nsub, (ctx + AD_WKEYS - 1) / AD_WKEYS);
   const float* p = partial + int64_t(bh) * nsub * AD_PSTR;
   // Loads that do not depend on the running max go out first: this thread's
@@ -782,19 +795,21 @@ extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, 
   return B * Hq * nsub * (D + 4);
 }
 
+// B query rows; chunk_start / qpb as in ad_ctx (nullptr / 1: one query per batch row).
 static int attn_decode_launch(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
-                              const int32_t* ctx_len, int64_t B, int64_t Hq, int64_t Hkv, int64_t S_max,
-                              int64_t max_ctx, float scale, float* partial, qmoe_bf16* out, hipStream_t s) {
+                              const int32_t* ctx_len, const int32_t* chunk_start, int64_t qpb, int64_t B,
+                              int64_t Hq, int64_t Hkv, int64_t S_max, int64_t max_ctx, float scale,
+                              float* partial, qmoe_bf16* out, hipStream_t s) {
   if (B == 0) return QMOE_OK;
   const int nsplit = int((max_ctx + AD_SPLIT - 1) / AD_SPLIT);
   const int nsub = nsplit * AD_SUBS;
   hipLaunchKernelGGL(attn_decode_split_kernel, dim3(unsigned(nsplit), unsigned(Hkv), unsigned(B)),
-                     dim3(AD_SUBS * 64), 0, s, q, k_cache, v_cache, ctx_len, int(Hq), int(Hkv), int(S_max),
-                     int(max_ctx), nsub, scale, partial);
+                     dim3(AD_SUBS * 64), 0, s, q, k_cache, v_cache, ctx_len, chunk_start, int(qpb), int(Hq),
+                     int(Hkv), int(S_max), int(max_ctx), nsub, scale, partial);
   int rc = hip_status("qmoe_attn_decode(split)");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(unsigned(B * Hq)), dim3(HD), 0, s, partial, ctx_len,
-                     int(Hq), int(max_ctx), nsub, out);
+                     chunk_start, int(qpb), int(S_max), int(Hq), int(max_ctx), nsub, out);
   return hip_status("qmoe_attn_decode(merge)");
 }
 
@@ -807,7 +822,7 @@ extern "C" int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536,
                "qmoe_attn_decode: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
   QMOE_REQUIRE(B >= 0 && B < 65536 && S_max > 0 && S_max < (1ll << 30), "qmoe_attn_decode: bad B/S_max");
-  return attn_decode_launch(q, k_cache, v_cache, ctx_len, B, Hq, Hkv, S_max, S_max, scale, partial, out,
+  return attn_decode_launch(q, k_cache, v_cache, ctx_len, nullptr, 1, B, Hq, Hkv, S_max, S_max, scale, partial, out,
                             as_stream(stream));
 }
 
@@ -821,6 +836,21 @@ extern "C" int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_ca
                "qmoe_attn_decode_bucket: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
   QMOE_REQUIRE(B >= 0 && B < 65536 && S_max > 0 && S_max < (1ll << 30), "qmoe_attn_decode_bucket: bad B/S_max");
   QMOE_REQUIRE(max_ctx > 0 && max_ctx <= S_max, "qmoe_attn_decode_bucket: need 0 < max_ctx <= S_max");
-  return attn_decode_launch(q, k_cache, v_cache, ctx_len, B, Hq, Hkv, S_max, max_ctx, scale, partial, out,
+  return attn_decode_launch(q, k_cache, v_cache, ctx_len, nullptr, 1, B, Hq, Hkv, S_max, max_ctx, scale, partial, out,
                             as_stream(stream));
+}
+
+
+extern "C" int qmoe_attn_decode_chunk(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                                      const int32_t* start, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
+                                      int64_t D, int64_t S_max, float scale, float* partial, qmoe_bf16* out,
+                                      qmoe_stream_t stream) {
+  QMOE_REQUIRE(q && k_cache && v_cache && start && partial && out, "qmoe_attn_decode_chunk: null pointer");
+  QMOE_REQUIRE(D == HD, "qmoe_attn_decode_chunk: head_dim must be 128");
+  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536,
+               "qmoe_attn_decode_chunk: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
+  QMOE_REQUIRE(B >= 0 && S > 0 && B * S < 65536 && S_max >= S && S_max < (1ll << 30),
+               "qmoe_attn_decode_chunk: bad B/S/S_max");
+  return attn_decode_launch(q, k_cache, v_cache, nullptr, start, S, B * S, Hq, Hkv, S_max, S_max, scale, partial,
+                            out, as_stream(stream));
 }

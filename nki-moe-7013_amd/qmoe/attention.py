@@ -25,6 +25,11 @@ def rope_tables(head_dim: int, max_pos: int, theta: float, device) -> tuple:
     return freqs.cos().contiguous(), freqs.sin().contiguous()
 
 
+# Chunks of up to this many query rows at a device-held start run as
+# single-query decode problems (qmoe_attn_decode_chunk).
+CHUNK_DECODE_MAX = 16
+
+
 class KVCache:
     """Contiguous K/V cache of one layer: ``[B, Hkv, S_max, D]`` bf16 each."""
 
@@ -77,7 +82,16 @@ class Attention:
         else:
             q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
                                   self.n_q, self.n_kv, cache.k, cache.v, self.eps, workspace=qws)
-        if S > 1:
+        if S > 1 and isinstance(start, torch.Tensor) and B * S <= CHUNK_DECODE_MAX:
+            # a few-token chunk at a device-held position (speculative verification):
+            # one decode problem per query spreads the K/V stream over many CUs
+            ws = self._ws.get(("chunk", B * S, cache.capacity))
+            if ws is None:
+                ws = ops.attn_decode_workspace(B * S, self.n_q, self.head_dim, cache.capacity, x.device)
+                self._ws[("chunk", B * S, cache.capacity)] = ws
+            o = ops.attn_decode_chunk(q.view(B * S, self.n_q, self.head_dim), cache.k, cache.v, B, S, start,
+                                      self.scale, ws)
+        elif S > 1:
             o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
         else:
             if ctx_len is None:

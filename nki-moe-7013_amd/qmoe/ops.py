@@ -530,6 +530,42 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return out
 
 
+def attn_decode_chunk(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, B: int, S: int,
+                      start: torch.Tensor, scale: Optional[float] = None,
+                      workspace: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of a short chunk ``q[B*S, Hq, D]`` at cache positions
+    ``start .. start+S-1`` (``start``: int32 ``[1]`` device tensor, clamped
+    into ``[0, S_max - S]``) as ``B*S`` single-query decode problems; returns
+    ``[B*S, Hq*D]``, the same values :func:`attn_prefill` computes (to
+    rounding)."""
+    T, Hq, D = q.shape
+    if T != B * S:
+        raise ValueError("q must be [B*S, Hq, D]")
+    _need(q, "q", BF16)
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[3] != D:
+        raise ValueError("k_cache must be [B, Hkv, S_max, D]")
+    Hkv, S_max = k_cache.shape[1], k_cache.shape[2]
+    _need(start, "start", I32, (1,))
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    need = int(lib().qmoe_attn_decode_workspace(T, Hq, D, S_max))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=F32, device=q.device)
+    if workspace.dtype != F32 or workspace.numel() < need or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous float32 tensor of >= {need} elements")
+    out = torch.empty(T, Hq * D, dtype=BF16, device=q.device) if out is None else out
+    _need(out, "out", BF16, (T, Hq * D))
+    _same_device(q, k_cache, v_cache, start, workspace, out)
+    check(
+        lib().qmoe_attn_decode_chunk(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(start), B, S, Hq, Hkv, D, S_max,
+                                     float(scale), _ptr(workspace), _ptr(out), _stream()),
+        "qmoe_attn_decode_chunk",
+    )
+    return out
+
+
 def attn_decode_workspace(B: int, Hq: int, D: int, S_max: int, device) -> torch.Tensor:
     n = int(lib().qmoe_attn_decode_workspace(B, Hq, D, S_max))
     return torch.empty(n, dtype=F32, device=device)

@@ -55,6 +55,8 @@ def test_version():
         (lambda l: l.qmoe_embed(1, 100, 6, 1, 1, 1, 1, None), "H % 4 == 0"),
         (lambda l: l.qmoe_embed(None, 100, 8, 1, 1, 1, 1, None), "null pointer"),
         (lambda l: l.qmoe_argmax(1, 2, 100, 100, 1, 8, 1, None), "workspace too small"),
+        (lambda l: l.qmoe_attn_decode_chunk(1, 1, 1, None, 1, 5, 32, 4, 128, 64, 0.1, 1, 1, None), "null pointer"),
+        (lambda l: l.qmoe_attn_decode_chunk(1, 1, 1, 1, 1, 5, 32, 4, 128, 4, 0.1, 1, 1, None), "bad B/S/S_max"),
         (lambda l: l.qmoe_argmax(1, 2, 100, 50, 1, 1 << 20, 1, None), "bad rows/n/ldx"),
         # decode block: x, h, rms_w, eps, w_router, bias, w13, w2, residual, T, H, I, E, k,
         #   logits, topk_idx, topk_w, workspace, workspace_bytes, x_out, out, stream

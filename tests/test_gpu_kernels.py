@@ -527,6 +527,47 @@ def test_attn_prefill_device_start(dev, B, S, start):
         assert torch.equal(out, ops.attn_prefill(q, kc, vc, B, S, p))
 
 
+@pytest.mark.parametrize("B,S,start", [(1, 5, 0), (1, 5, 700), (2, 3, 130), (1, 16, 63)])
+def test_attn_decode_chunk(dev, B, S, start):
+    """Few-token chunks at a device-held start as single-query decode problems
+    (qmoe_attn_decode_chunk): against the oracle and the tiled prefill kernel,
+    and in a captured graph replayed at two positions (including the clamp of
+    a start past S_max - S)."""
+    announce(f"attn_decode_chunk B={B} S={S} start={start}")
+    S_max = start + S + 40
+    g = torch.Generator(device=dev).manual_seed(3 * S + start)
+    q = bf16_randn((B * S, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    st = torch.tensor([start], dtype=torch.int32, device=dev)
+    got = ops.attn_decode_chunk(q, kc, vc, B, S, st)
+    tiled = ops.attn_prefill(q, kc, vc, B, S, start)
+    torch.cuda.synchronize()
+    pos = torch.tensor([list(range(start, start + S))] * B)
+    ref = oracle.gqa_attention(q.cpu().view(B, S, HQ, D).transpose(1, 2), kc.cpu()[:, :, : start + S],
+                               vc.cpu()[:, :, : start + S], pos)
+    assert_close_layer(got.cpu().view(B, S, HQ, D), ref, "attn_decode_chunk", max_abs_tol=1e-2,
+                       mean_rel_tol=5e-3)
+    assert float((got.float() - tiled.float()).abs().max()) <= 1e-2
+    ws = ops.attn_decode_workspace(B * S, HQ, D, S_max, dev)
+    out = torch.empty_like(got)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.attn_decode_chunk(q, kc, vc, B, S, st, workspace=ws, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.attn_decode_chunk(q, kc, vc, B, S, st, workspace=ws, out=out)
+    for p, eff in ((start + 17, start + 17), (start, start), (S_max, S_max - S)):
+        st.fill_(p)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = ops.attn_decode_chunk(q, kc, vc, B, S, torch.tensor([eff], dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 @pytest.mark.parametrize("ctx", [[1], [300, 1000, 17], [8192] * 2])
 def test_attn_decode(dev, ctx):
     announce(f"attn_decode ctx={ctx}")
