@@ -106,7 +106,9 @@ int qmoe_moe_permute(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E,
 
 /* Rows of `tiles` for which qmoe_moe_permute / qmoe_moe_route spread the
  * placement over several workgroups: ceil(T*k / tile_m) + E + ceil(C*(E+1)/4)
- * with C = ceil(T*k / 1024) chunks (-1 for a non-positive k, E or tile_m).
+ * with C = ceil(T*k / 1024) chunks when 4096 < T*k <= 4096 * 1024 (the sizes
+ * that path covers), else ceil(T*k / tile_m) + E (-1 for a non-positive k, E
+ * or tile_m).
  * Replaces: nothing in the reference (a sizing helper of this library). */
 int64_t qmoe_moe_permute_tiles(int64_t T, int64_t k, int64_t E, int64_t tile_m);
 

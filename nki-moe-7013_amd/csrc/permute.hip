@@ -28,10 +28,13 @@ constexpr int PERM_MAX_CHUNKS = 4096;     // chunk counts summed per expert thre
 constexpr int PERM_ONE_WG_MAX = 4096;     // pairs handled by the single-workgroup kernel
 
 // Rows of `tiles` the two-launch path needs: the tile table bound plus the
-// scratch (per chunk: E counts and one flag, four ints per row).
+// scratch (per chunk: E counts and one flag, four ints per row); just the
+// bound where that path is not taken (too few or too many chunks).
 int64_t permute_tiles_rows(int64_t N, int64_t E, int64_t tile_m) {
   const int64_t nchunks = (N + PERM_CHUNK - 1) / PERM_CHUNK;
-  return (N + tile_m - 1) / tile_m + E + (nchunks * (E + 1) + 3) / 4;
+  const int64_t need = (N + tile_m - 1) / tile_m + E;
+  if (N <= PERM_ONE_WG_MAX || nchunks > PERM_MAX_CHUNKS) return need;
+  return need + (nchunks * (E + 1) + 3) / 4;
 }
 
 __global__ __launch_bounds__(PERM_THREADS) void permute_rank_kernel(

@@ -115,11 +115,14 @@ def test_decode_block_workspace_size():
 
 def test_permute_tiles_rows():
     """Rows of `tiles` for the per-chunk permutation: the tile-table bound
-    ceil(T*k/tile_m) + E, then (E + 1) ints of scratch per 1024-pair chunk."""
+    ceil(T*k/tile_m) + E, then (E + 1) ints of scratch per 1024-pair chunk
+    where that path runs (4096 < T*k <= 4096 chunks of 1024)."""
     l = _lib.lib()
     assert l.qmoe_moe_permute_tiles(4096, 8, 128, 256) == 128 + 128 + (32 * 129 + 3) // 4
     assert l.qmoe_moe_permute_tiles(513, 8, 128, 128) == 33 + 128 + (5 * 129 + 3) // 4
     assert l.qmoe_moe_permute_tiles(0, 8, 128, 128) == 128
+    assert l.qmoe_moe_permute_tiles(512, 8, 128, 128) == 32 + 128  # one workgroup: no scratch
+    assert l.qmoe_moe_permute_tiles(1 << 20, 8, 128, 256) == (1 << 15) + 128  # beyond 4096 chunks
     assert l.qmoe_moe_permute_tiles(4, 8, 128, 0) == -1
 
 
