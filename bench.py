@@ -641,7 +641,7 @@ def main():
         "moe_block_GBps": round(dec["block_GBps"], 1),
         "moe_block_hbm_frac": round(dec["block_frac"], 4),
         "moe_block_us_spread": dec["us_per_block_spread"],
-        # the north-star companions: prefill MoE block (T=4096, Zipf-skewed
+        # the companion workloads: prefill MoE block (T=4096, Zipf-skewed
         # routing) and the full 48-layer model at batch 1 (child process)
         "prefill_moe_block_tokens_per_s": (round(extra["prefill_T4096"]["tokens_per_s"], 1)
                                            if "prefill_T4096" in extra else None),
