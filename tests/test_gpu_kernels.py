@@ -477,7 +477,8 @@ def test_qkv_finish_matches_qkv_norm_rope(dev, attn_w):
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
 
 
-@pytest.mark.parametrize("ctx,bucket", [([1], 256), ([300, 1000, 17], 1024), ([256], 256)])
+@pytest.mark.parametrize("ctx,bucket", [([1], 256), ([300, 1000, 17], 1024), ([256], 256),
+                                        ([1000, 17, 640, 1024, 5, 900, 128, 129], 1024)])
 def test_attn_decode_bucket(dev, ctx, bucket):
     """A launch sized for a context bucket gives the same bits as the one sized
     for the whole cache (S_max 2048): the live splits and the merge are the
@@ -568,7 +569,8 @@ def test_attn_decode_chunk(dev, B, S, start):
         assert torch.equal(out, eager)
 
 
-@pytest.mark.parametrize("ctx", [[1], [300, 1000, 17], [8192] * 2])
+# batch 8 with contexts that end on, just past and inside 64-key splits
+@pytest.mark.parametrize("ctx", [[1], [300, 1000, 17], [8192] * 2, [1, 64, 65, 128, 129, 700, 1000, 2048]])
 def test_attn_decode(dev, ctx):
     announce(f"attn_decode ctx={ctx}")
     B = len(ctx)
