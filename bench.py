@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--extra", action="store_true",
-                    help="also time T=8/64 decode and the attention layer")
+                    help="time T=8/64 decode and the attention layer (the default; kept for old command lines)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the T=8/64 decode and attention-layer timings")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 PMC traffic runs")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-prefill", action="store_true", help="skip the T=4096 prefill MoE block")
@@ -596,7 +597,7 @@ def main():
     if not a.no_prefill:
         extra["prefill_T4096"] = bench_prefill(layers, dev)
         print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
-    if a.extra:
+    if not a.no_extra:
         for T in (8, 64):
             extra[f"decode_T{T}"] = bench_decode(layers, T, 480, 48, dev)
             print(f"[bench] decode T={T}: {extra[f'decode_T{T}']}", file=sys.stderr, flush=True)
