@@ -57,6 +57,10 @@ typedef void* qmoe_stream_t;
  * the size of its partial-output workspace. */
 #define QMOE_DECODE_BLOCK_WGS 256
 
+/* Largest T * H qmoe_moe_decode_block_noalloc accepts (its static scratch is
+ * QMOE_DECODE_BLOCK_WGS * this many floats = 16 MiB per GPU). */
+#define QMOE_DECODE_BLOCK_NOALLOC_MAX_TH 16384
+
 int qmoe_version(void);
 const char* qmoe_last_error(void);
 
@@ -156,6 +160,27 @@ int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* r
  * Replaces: nothing in the reference (its kernels allocate their own HBM
  *   scratch, e.g. qwen_with_nki.py:1858); the caller owns memory here. */
 int64_t qmoe_moe_decode_block_workspace(int64_t T, int64_t H);
+
+/* qmoe_moe_decode_block without the workspace argument: the partial outputs
+ * go to a static device array inside the library (16 MiB, one copy per GPU,
+ * held until the process ends), so this call allocates nothing, not even on
+ * its first use on a device.  Same arguments, kernels, limits and results as
+ * qmoe_moe_decode_block, plus T * H <= QMOE_DECODE_BLOCK_NOALLOC_MAX_TH (T <= 8
+ * at H = 2048); larger sizes are rejected with QMOE_ERR_INVALID.  The device is
+ * the current device, which must be the stream's.  Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (other streams,
+ * other host threads) race and must be ordered by the caller.  Nothing needs
+ * clearing between calls (each call overwrites all the partials it reads).
+ * Replaces: nothing in the reference (no counterpart); it is for callers that
+ *   cannot allocate device memory (code under HIP graph capture, tight
+ *   serving loops, harnesses that forbid hipMalloc). */
+int qmoe_moe_decode_block_noalloc(const qmoe_bf16* x, const float* h, const qmoe_bf16* rms_w,
+                                  float eps, const qmoe_bf16* w_router, const float* bias,
+                                  const qmoe_bf16* w13, const qmoe_bf16* w2,
+                                  const float* residual, int64_t T, int64_t H, int64_t I,
+                                  int64_t E, int64_t k, float* logits, int32_t* topk_idx,
+                                  float* topk_w, qmoe_bf16* x_out, float* out,
+                                  qmoe_stream_t stream);
 
 /* Decode expert MLPs without the combine (bandwidth-bound GEMV form; each
  * touched expert's weights are streamed once for all tokens routed to it).

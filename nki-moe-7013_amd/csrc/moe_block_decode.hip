@@ -30,6 +30,9 @@
 // HBM traffic is the touched experts' weights (U * 3 * H * I * 2 bytes) plus
 // the router (E * H * 2); the partials are BLK_WGS * T * H * 4 bytes (2 MB at
 // T = 1), written once and read once.
+#include <atomic>
+#include <mutex>
+
 #include "decode_util.hpp"
 #include "topk_impl.hpp"
 
@@ -390,6 +393,96 @@ static void launch_block_experts(const uint16_t* x, const float* logits, int64_t
                                                                w13, w2b, T, H, I, partial, s);
 }
 
+// Argument checks shared by both entry points (everything but the partials).
+static int check_block_args(const char* fn, const qmoe_bf16* x, const float* h,
+                            const qmoe_bf16* rms_w, float eps, const qmoe_bf16* w_router,
+                            const qmoe_bf16* w13, const qmoe_bf16* w2, int64_t T, int64_t H,
+                            int64_t I, int64_t E, int64_t k, const float* logits,
+                            const int32_t* topk_idx, const float* topk_w, const qmoe_bf16* x_out,
+                            const float* out) {
+  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && out, "%s: null pointer", fn);
+  QMOE_REQUIRE((x != nullptr) != (h != nullptr), "%s: pass exactly one of x and h", fn);
+  QMOE_REQUIRE(!h || (rms_w && x_out), "%s: h needs rms_w and x_out", fn);
+  QMOE_REQUIRE(T >= 0 && T <= BLK_MAX_T, "%s: T must be <= 8 (T=%lld)", fn, (long long)T);
+  QMOE_REQUIRE(E > 0 && E <= ROUTER_MAX_E && k > 0 && k <= ROUTER_MAX_K && k <= E && T * k <= BLK_MAX_PAIRS,
+               "%s: need E <= 256, k <= min(16, E), T*k <= 64", fn);
+  QMOE_REQUIRE(H >= 512 && H <= 4096 && H % 512 == 0 && (H / 512 & (H / 512 - 1)) == 0,
+               "%s: H must be 512, 1024, 2048 or 4096", fn);
+  QMOE_REQUIRE(I % QMOE_W13_GROUP == 0 && I > 0 && I <= 1536, "%s: I must be a multiple of 32, <= 1536",
+               fn);
+  QMOE_REQUIRE(eps >= 0.0f, "%s: eps < 0", fn);
+  return QMOE_OK;
+}
+
+// The three launches, on validated arguments; `partial` holds BLK_WGS * T * H
+// floats, every one of which the expert kernel overwrites before the reduce
+// reads it (no clearing needed between calls).
+static int run_block(const char* fn, const qmoe_bf16* x, const float* h, const qmoe_bf16* rms_w,
+                     float eps, const qmoe_bf16* w_router, const float* bias, const qmoe_bf16* w13,
+                     const qmoe_bf16* w2, const float* residual, int64_t T, int64_t H, int64_t I,
+                     int64_t E, int64_t k, float* logits, int32_t* topk_idx, float* topk_w,
+                     float* partial, qmoe_bf16* x_out, float* out, hipStream_t s) {
+  if (T == 0) return QMOE_OK;
+  const uint16_t* xin = h ? x_out : x;
+  switch (H / 512) {
+#define QMOE_BLK(HC)                                                                              \
+  case HC:                                                                                        \
+    hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(64), 0, s, x, h, rms_w,    \
+                       eps, w_router, bias, int(T), int(H), int(E), logits, x_out);               \
+    if (int rc = hip_status(fn)) return rc;                                                       \
+    launch_block_experts<HC>(xin, logits, E, k, topk_idx, topk_w, w13, w2, T, H, I, partial, s);  \
+    break;
+    QMOE_BLK(1)
+    QMOE_BLK(2)
+    QMOE_BLK(4)
+    QMOE_BLK(8)
+#undef QMOE_BLK
+  }
+  if (int rc = hip_status(fn)) return rc;
+  hipLaunchKernelGGL(block_reduce_kernel, dim3(unsigned(H / 64), unsigned(T)), dim3(64 * BLK_RED_WAVES),
+                     0, s, partial, residual, int(T), int(H), out);
+  return hip_status(fn);
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+// The partials of qmoe_moe_decode_block_noalloc live in this fixed array of
+// the library's device memory (16 MiB; each GPU holds its own copy until the
+// process ends).  Host code never passes `scratch` itself to a kernel: on the
+// host that name is only a stand-in, so its device address is looked up once
+// per device with hipGetSymbolAddress and kept in g_scratch.
+constexpr int64_t BLK_NOALLOC_FLOATS = int64_t(BLK_WGS) * QMOE_DECODE_BLOCK_NOALLOC_MAX_TH;
+static __device__ __align__(256) float scratch[BLK_NOALLOC_FLOATS];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static std::atomic<float*> g_scratch[SCRATCH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch` (resolved on the first
+// call on that device, with that device current).
+static int scratch_on_current_device(const char* fn, float** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(QMOE_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  QMOE_REQUIRE(dev >= 0 && dev < SCRATCH_MAX_DEVICES, "%s: device %d beyond %d", fn, dev,
+               SCRATCH_MAX_DEVICES);
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr)
+        return fail(QMOE_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                    hipGetErrorString(e));
+      p = static_cast<float*>(addr);
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return QMOE_OK;
+}
+
 }  // namespace qmoe
 
 using namespace qmoe;
@@ -406,41 +499,35 @@ extern "C" int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const q
                                      int64_t E, int64_t k, float* logits, int32_t* topk_idx,
                                      float* topk_w, void* workspace, int64_t workspace_bytes,
                                      qmoe_bf16* x_out, float* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && workspace && out,
-               "qmoe_moe_decode_block: null pointer");
-  QMOE_REQUIRE((x != nullptr) != (h != nullptr), "qmoe_moe_decode_block: pass exactly one of x and h");
-  QMOE_REQUIRE(!h || (rms_w && x_out), "qmoe_moe_decode_block: h needs rms_w and x_out");
-  QMOE_REQUIRE(T >= 0 && T <= BLK_MAX_T, "qmoe_moe_decode_block: T must be <= 8 (T=%lld)", (long long)T);
-  QMOE_REQUIRE(E > 0 && E <= ROUTER_MAX_E && k > 0 && k <= ROUTER_MAX_K && k <= E && T * k <= BLK_MAX_PAIRS,
-               "qmoe_moe_decode_block: need E <= 256, k <= min(16, E), T*k <= 64");
-  QMOE_REQUIRE(H >= 512 && H <= 4096 && H % 512 == 0 && (H / 512 & (H / 512 - 1)) == 0,
-               "qmoe_moe_decode_block: H must be 512, 1024, 2048 or 4096");
-  QMOE_REQUIRE(I % QMOE_W13_GROUP == 0 && I > 0 && I <= 1536,
-               "qmoe_moe_decode_block: I must be a multiple of 32, <= 1536");
-  QMOE_REQUIRE(eps >= 0.0f, "qmoe_moe_decode_block: eps < 0");
+  const char* fn = "qmoe_moe_decode_block";
+  if (int rc = check_block_args(fn, x, h, rms_w, eps, w_router, w13, w2, T, H, I, E, k, logits,
+                                topk_idx, topk_w, x_out, out))
+    return rc;
+  QMOE_REQUIRE(workspace, "%s: null workspace", fn);
   QMOE_REQUIRE(workspace_bytes >= qmoe_moe_decode_block_workspace(T, H),
-               "qmoe_moe_decode_block: workspace of %lld bytes < %lld", (long long)workspace_bytes,
+               "%s: workspace of %lld bytes < %lld", fn, (long long)workspace_bytes,
                (long long)qmoe_moe_decode_block_workspace(T, H));
-  if (T == 0) return QMOE_OK;
-  hipStream_t s = as_stream(stream);
-  const uint16_t* xin = h ? x_out : x;
-  float* partial = static_cast<float*>(workspace);
-  switch (H / 512) {
-#define QMOE_BLK(HC)                                                                              \
-  case HC:                                                                                        \
-    hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(64), 0, s, x, h, rms_w,    \
-                       eps, w_router, bias, int(T), int(H), int(E), logits, x_out);               \
-    if (int rc = hip_status("qmoe_moe_decode_block(router)")) return rc;                          \
-    launch_block_experts<HC>(xin, logits, E, k, topk_idx, topk_w, w13, w2, T, H, I, partial, s);  \
-    break;
-    QMOE_BLK(1)
-    QMOE_BLK(2)
-    QMOE_BLK(4)
-    QMOE_BLK(8)
-#undef QMOE_BLK
-  }
-  if (int rc = hip_status("qmoe_moe_decode_block(experts)")) return rc;
-  hipLaunchKernelGGL(block_reduce_kernel, dim3(unsigned(H / 64), unsigned(T)), dim3(64 * BLK_RED_WAVES),
-                     0, s, partial, residual, int(T), int(H), out);
-  return hip_status("qmoe_moe_decode_block(reduce)");
+  return run_block(fn, x, h, rms_w, eps, w_router, bias, w13, w2, residual, T, H, I, E, k, logits,
+                   topk_idx, topk_w, static_cast<float*>(workspace), x_out, out, as_stream(stream));
+}
+
+extern "C" int qmoe_moe_decode_block_noalloc(const qmoe_bf16* x, const float* h,
+                                             const qmoe_bf16* rms_w, float eps,
+                                             const qmoe_bf16* w_router, const float* bias,
+                                             const qmoe_bf16* w13, const qmoe_bf16* w2,
+                                             const float* residual, int64_t T, int64_t H,
+                                             int64_t I, int64_t E, int64_t k, float* logits,
+                                             int32_t* topk_idx, float* topk_w, qmoe_bf16* x_out,
+                                             float* out, qmoe_stream_t stream) {
+  const char* fn = "qmoe_moe_decode_block_noalloc";
+  if (int rc = check_block_args(fn, x, h, rms_w, eps, w_router, w13, w2, T, H, I, E, k, logits,
+                                topk_idx, topk_w, x_out, out))
+    return rc;
+  QMOE_REQUIRE(T * H <= QMOE_DECODE_BLOCK_NOALLOC_MAX_TH,
+               "%s: T*H = %lld exceeds the static scratch limit of %d (T <= 8 at H = 2048)", fn,
+               (long long)(T * H), QMOE_DECODE_BLOCK_NOALLOC_MAX_TH);
+  float* partial = nullptr;
+  if (int rc = scratch_on_current_device(fn, &partial)) return rc;
+  return run_block(fn, x, h, rms_w, eps, w_router, bias, w13, w2, residual, T, H, I, E, k, logits,
+                   topk_idx, topk_w, partial, x_out, out, as_stream(stream));
 }

@@ -23,6 +23,7 @@ W13_GROUP = 32
 W2_BLOCK = 8
 GROUPED_MAX_TILE_M = 256
 DECODE_BLOCK_WGS = 256
+DECODE_BLOCK_NOALLOC_MAX_TH = 16384
 
 P = c_void_p
 I64 = c_int64
@@ -39,6 +40,8 @@ PROTOTYPES = {
     "qmoe_moe_decode_block": (
         c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, P, P, P]),
     "qmoe_moe_decode_block_workspace": (c_int64, [I64, I64]),
+    "qmoe_moe_decode_block_noalloc": (
+        c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, P, P]),
     "qmoe_moe_experts_gemv": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_experts_grouped": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_combine": (c_int, [P, c_int, P, P, P, I64, I64, I64, P, P]),

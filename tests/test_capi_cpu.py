@@ -68,6 +68,13 @@ def test_version():
                                            1, 1, 1, 1, 1 << 30, None, 1, None), "exactly one"),
         (lambda l: l.qmoe_moe_decode_block(1, None, None, 1e-6, 1, None, 1, 1, None, 1, 2048, 100, 128, 8,
                                            1, 1, 1, 1, 1 << 30, None, 1, None), "multiple of 32"),
+        # allocation-free decode block: same arguments without workspace / workspace_bytes
+        (lambda l: l.qmoe_moe_decode_block_noalloc(1, None, None, 1e-6, 1, None, 1, 1, None, 8, 4096, 768, 128, 8,
+                                                   1, 1, 1, None, 1, None), "static scratch limit"),
+        (lambda l: l.qmoe_moe_decode_block_noalloc(1, None, None, 1e-6, 1, None, 1, 1, None, 9, 1024, 768, 128, 8,
+                                                   1, 1, 1, None, 1, None), "T must be"),
+        (lambda l: l.qmoe_moe_decode_block_noalloc(1, None, None, 1e-6, None, None, 1, 1, None, 1, 2048, 768, 128, 8,
+                                                   1, 1, 1, None, 1, None), "null pointer"),
         (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 1, 1, 2048, 32, 4, 64, 10, 1e-6, 1, 1, 1, 1, None), "head_dim"),
         (lambda l: l.qmoe_qkv_norm_rope(1, 1, 1, 1, 1, 1, 10, 1, 8, 1, 2048, 32, 4, 128, 10, 1e-6, 1, 1, 1, None, None),
          "needs the workspace"),
