@@ -31,15 +31,46 @@ CHUNK_DECODE_MAX = 16
 
 
 class KVCache:
-    """Contiguous K/V cache of one layer: ``[B, Hkv, S_max, D]`` bf16 each."""
+    """Contiguous K/V cache of one layer: ``[B, Hkv, S_max, D]`` bf16 each.
+
+    Unpacks like the reference's ``(K, V)`` present-key-value tuple
+    (``k, v = cache``), and :meth:`wrap` takes such a tuple back without a copy."""
 
     def __init__(self, B: int, n_kv: int, S_max: int, head_dim: int, device):
         self.k = torch.zeros(B, n_kv, S_max, head_dim, dtype=torch.bfloat16, device=device)
         self.v = torch.zeros_like(self.k)
 
+    @classmethod
+    def wrap(cls, kv) -> "KVCache":
+        """A :class:`KVCache` as is, or a ``(K, V)`` pair of contiguous bf16
+        ``[B, Hkv, S_max, D]`` device tensors viewed as one (no copy)."""
+        if isinstance(kv, KVCache):
+            return kv
+        if not isinstance(kv, (tuple, list)) or len(kv) != 2:
+            raise ValueError("past_key_value must be a KVCache or a (K, V) pair")
+        k, v = kv
+        for name, t in (("K", k), ("V", v)):
+            if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.dim() != 4 \
+                    or not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError(f"past_key_value {name} must be a contiguous bf16 [B, Hkv, S_max, D] GPU tensor")
+        if k.shape != v.shape:
+            raise ValueError("past_key_value K and V shapes differ")
+        c = cls.__new__(cls)
+        c.k, c.v = k, v
+        return c
+
     @property
     def capacity(self) -> int:
         return self.k.shape[2]
+
+    def __iter__(self):
+        return iter((self.k, self.v))
+
+    def __len__(self) -> int:
+        return 2
+
+    def __getitem__(self, i):
+        return (self.k, self.v)[i]
 
 
 class Attention:

@@ -82,15 +82,18 @@ def prepare_inference(model_cls, args):
 
 
 def run_generation(model, tokenizer, prompts, generation_config, prompt_ids: Optional[torch.Tensor] = None):
-    """main.py:634-649."""
+    """main.py:634-649.  Text prompts are right-padded to the longest
+    (main.py:366) and their attention mask goes to ``generate``, so each row
+    continues from its own last real token."""
+    attention_mask = None
     if prompt_ids is None:
         if tokenizer is None:
             raise ValueError("text prompts need a tokenizer (local --model-path); use --prompt-ids")
         enc = tokenizer(prompts, padding=True, return_tensors="pt")
-        prompt_ids = enc.input_ids
+        prompt_ids, attention_mask = enc.input_ids, enc.attention_mask
     adapter = HuggingFaceGenerationAdapter(model)
     t0 = time.perf_counter()
-    out = adapter.generate(prompt_ids, generation_config=generation_config,
+    out = adapter.generate(prompt_ids, attention_mask=attention_mask, generation_config=generation_config,
                            max_length=model.neuron_config.max_length)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
@@ -113,7 +116,7 @@ def main(argv=None):
     elif args.random_prompt_len:
         g = torch.Generator().manual_seed(args.seed)
         ids = torch.randint(0, model.config.vocab_size, (args.batch_size, args.random_prompt_len), generator=g)
-    run_generation(model, tok, args.prompts, gen, ids)
+    return run_generation(model, tok, args.prompts, gen, ids)
 
 
 if __name__ == "__main__":

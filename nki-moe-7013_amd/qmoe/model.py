@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import json
 import os
+from collections.abc import Mapping
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Any, Callable, Dict, List, Optional
@@ -134,17 +135,33 @@ class RMSNormWeight:
 class NeuronQwen3MoeDecoderLayer:
     """``h = x + Attn(RMSNorm_in(x)); out = h + MoE(RMSNorm_post(h))``
     (qwen_with_nki.py:10155-10213).  The residual stream is fp32; both
-    residual adds are fused into kernel epilogues."""
+    residual adds are fused into kernel epilogues.
 
-    def __init__(self, config: Qwen3MoeInferenceConfig, layer_idx: int, w: Dict[str, torch.Tensor]):
+    ``NeuronQwen3MoeDecoderLayer(config, layer_idx)`` builds the layer with
+    seeded random-init weights on the current GPU, as the reference's
+    constructor (10113-10153) creates its own parameters; pass ``w`` (one
+    layer of :func:`random_params` or of the checkpoint converter) to use
+    given weights."""
+
+    def __init__(self, config: Qwen3MoeInferenceConfig, layer_idx: int,
+                 w: Optional[Dict[str, torch.Tensor]] = None):
         c = config
+        if w is None:
+            if not torch.cuda.is_available():
+                raise RuntimeError("no GPU visible: this layer runs only on an MI355X")
+            dev = torch.device("cuda", torch.cuda.current_device())
+            seed = int(getattr(c.neuron_config, "seed", 0)) * 1000003 + int(layer_idx)
+            w = random_layer_params(c, dev, torch.Generator(device=dev).manual_seed(seed))
+        self.config = c
         self.layer_idx = layer_idx
+        self.hidden_size = c.hidden_size
         self.input_layernorm = RMSNormWeight(w["input_layernorm"], c.rms_norm_eps)
         self.post_attention_layernorm = RMSNormWeight(w["post_attention_layernorm"], c.rms_norm_eps)
         self.self_attn = Attention(w["wqkv"], w["q_norm"], w["k_norm"], w["wo"], c.num_attention_heads,
                                    c.num_key_value_heads, c.head_dim, c.rms_norm_eps)
         self.mlp = MoEBlock(w["router"], w["w13"], w["w2"], c.num_experts_per_tok)
         self.cache: Optional[KVCache] = None
+        self._rope = None  # (cos, sin) built from head_dim / rope_theta on first use
 
     def run(self, h: torch.Tensor, positions: torch.Tensor, B: int, S: int, rope, start=0,
             ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
@@ -161,22 +178,105 @@ class NeuronQwen3MoeDecoderLayer:
         self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
         return h
 
-    def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
-                past_key_value=None, padding_mask=None, rope=None, **kwargs):
-        """Reference layer contract: ``hidden_states[B,S,H]`` -> ``(hidden_states,
-        present_key_value, cos_cache, sin_cache, None)``; the KV cache is the
-        layer's contiguous cache (or ``past_key_value`` = a :class:`KVCache`)."""
+    def rope_tables(self, n_pos: int, device):
+        """cos/sin tables covering positions ``[0, n_pos)`` from the config's
+        head_dim and rope_theta (the reference's ``RotaryEmbedding``,
+        qwen_with_nki.py:10083-10087); grown in powers of two when needed."""
+        c = self.config
+        limit = int(getattr(c, "max_position_embeddings", n_pos))
+        if n_pos > limit:
+            raise ValueError(f"position {n_pos - 1} is beyond max_position_embeddings={limit}")
+        if self._rope is None or self._rope[0].shape[0] < n_pos or self._rope[0].device != device:
+            size = min(limit, max(256, 1 << (int(n_pos) - 1).bit_length()))
+            self._rope = rope_tables(c.head_dim, size, float(c.rope_theta), device)
+        return self._rope
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                position_ids: Optional[torch.Tensor] = None, past_key_value=None, padding_mask=None,
+                rope=None, **kwargs):
+        """The reference layer contract (qwen_with_nki.py:10155-10213):
+        ``hidden_states[B, S, H]`` -> ``(hidden_states, present_key_value,
+        cos_cache, sin_cache, None)``.
+
+        * ``position_ids[B, S]`` (default ``0..S-1``): row b holds consecutive
+          positions; a chunk with S > 1 starts at the same position in every
+          row; position == cache index.
+        * ``past_key_value``: a :class:`KVCache` or a ``(K, V)`` pair of bf16
+          ``[B, Hkv, S_max, D]`` tensors, updated in place.  Without it the
+          layer keeps its own cache, allocated on first use with room for
+          ``neuron_config.max_length + 1`` positions (reallocated by a chunk
+          that starts at position 0 and does not fit).
+        * ``attention_mask``: attention is causal over cache rows
+          ``[0, position]``; a mask is accepted when it says exactly that or
+          marks right padding (``[B, L]`` of 1s then 0s: rows past a
+          sequence's end only affect those rows' own outputs).  Any other mask
+          is rejected.
+        * ``rope``: optional ``(cos, sin)`` tables; by default the layer builds
+          them from ``head_dim`` and ``rope_theta``.
+
+        Returns ``hidden_states`` in the input dtype; ``present_key_value`` is
+        the cache, which unpacks as ``(K, V)``."""
+        if hidden_states.dim() != 3 or hidden_states.shape[2] != self.hidden_size:
+            raise ValueError(f"hidden_states must be [B, S, {self.hidden_size}]")
+        if not hidden_states.is_cuda:
+            raise ValueError("hidden_states must be on the GPU")
         B, S, H = hidden_states.shape
-        if past_key_value is not None:
-            self.cache = past_key_value
+        dev = hidden_states.device
         if position_ids is None:
-            position_ids = torch.arange(S, device=hidden_states.device).expand(B, S)
-        pos = position_ids.to(torch.int32).reshape(-1).contiguous()
-        start = int(position_ids[0, 0])
-        h = hidden_states.float().reshape(B * S, H).contiguous()
-        self.run(h, pos, B, S, rope, start)
+            position_ids = torch.arange(S, device=dev).expand(B, S)
+        if position_ids.shape != (B, S):
+            raise ValueError(f"position_ids must be [{B}, {S}]")
+        pos_cpu = position_ids.detach().to("cpu", torch.int64)
+        if bool((pos_cpu < 0).any()):
+            raise ValueError("position_ids must be non-negative")
+        if S > 1 and not torch.equal(pos_cpu, pos_cpu[:1, :1] + torch.arange(S).expand(B, S)):
+            raise ValueError("a chunk of S > 1 tokens needs positions start..start+S-1, the same in every row")
+        starts = pos_cpu[:, 0]
+        _check_causal_mask(attention_mask, pos_cpu)
+        end = int(pos_cpu.max()) + 1
+        if past_key_value is not None:
+            self.cache = KVCache.wrap(past_key_value)
+        elif (self.cache is None or self.cache.k.shape[0] != B or self.cache.capacity < end) and int(starts.min()) == 0:
+            cap = max(end, int(self.config.neuron_config.max_length) + 1)
+            self.cache = KVCache(B, self.config.num_key_value_heads, cap, self.config.head_dim, dev)
+        if self.cache is None or self.cache.k.shape[0] != B:
+            raise ValueError("no KV cache for this batch: start at position 0 or pass past_key_value")
+        if self.cache.capacity < end:
+            raise ValueError(f"position {end - 1} is beyond the KV cache capacity {self.cache.capacity}")
+        if rope is None:
+            rope = self.rope_tables(end, dev)
+        pos = position_ids.to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+        # the layer runs in place on its fp32 residual stream: always a copy,
+        # never the caller's tensor (an fp32 input would otherwise be overwritten)
+        h = hidden_states.reshape(B * S, H).to(torch.float32, copy=True).contiguous()
+        if S > 1:
+            self.run(h, pos, B, S, rope, int(starts[0]))
+        else:
+            self.run(h, pos, B, 1, rope, 0, ctx_len=(pos + 1).contiguous())
         out = h.view(B, S, H).to(hidden_states.dtype)
         return out, self.cache, rope[0], rope[1], None
+
+
+def _check_causal_mask(mask: Optional[torch.Tensor], pos: torch.Tensor) -> None:
+    """Accept ``None`` or a 2-D 0/1 mask ``[B, L]`` that is 1 up to a
+    sequence's length and 0 after it (right padding, main.py:366) and that
+    covers every query position; anything else would ask for attention the
+    causal cache kernels do not compute."""
+    if mask is None:
+        return
+    m = mask.detach().to("cpu")
+    B = pos.shape[0]
+    if m.dim() != 2 or m.shape[0] != B:
+        raise ValueError("attention_mask must be None or [B, L] (right padding); "
+                         "attention here is causal over the contiguous KV cache")
+    m = m.to(torch.int64)
+    if not bool(((m == 0) | (m == 1)).all()):
+        raise ValueError("attention_mask must hold 0/1")
+    lengths = m.sum(1)
+    prefix = torch.arange(m.shape[1]).expand_as(m) < lengths.unsqueeze(1)
+    if not torch.equal(m.bool(), prefix):
+        raise ValueError("attention_mask must be right-padded (1s then 0s); "
+                         "other masks are not supported by the causal cache kernels")
 
 
 class NeuronQwen3MoeModel:
@@ -220,11 +320,11 @@ class NeuronQwen3MoeModel:
         return ops.gemm(y, self.lm_head, _lib.GEMM_STORE_F32, out=out)
 
 
-def random_params(config: Qwen3MoeInferenceConfig, device, seed: int = 0, std: float = 0.02) -> Dict[str, Any]:
-    """Random-init bf16 weights of the model, generated on the GPU from ``seed``
-    (N(0, std) matrices; RMSNorm weights 1)."""
+def random_layer_params(config: Qwen3MoeInferenceConfig, device, g: torch.Generator,
+                        std: float = 0.02) -> Dict[str, torch.Tensor]:
+    """One decoder layer of random-init bf16 weights drawn from ``g`` on the
+    GPU (N(0, std) matrices; RMSNorm weights 1)."""
     c = config
-    g = torch.Generator(device=device).manual_seed(seed)
     H, D, E, I = c.hidden_size, c.head_dim, c.num_experts, c.moe_intermediate_size
     nq, nkv = c.num_attention_heads, c.num_key_value_heads
 
@@ -234,53 +334,135 @@ def random_params(config: Qwen3MoeInferenceConfig, device, seed: int = 0, std: f
     def ones(n):
         return torch.ones(n, dtype=torch.bfloat16, device=device)
 
-    layers = []
-    for _ in range(c.num_hidden_layers):
-        layers.append({
-            "input_layernorm": ones(H), "post_attention_layernorm": ones(H),
-            "wqkv": rnd((nq + 2 * nkv) * D, H), "q_norm": ones(D), "k_norm": ones(D),
-            "wo": rnd(H, nq * D), "router": rnd(E, H),
-            "w13": rnd(E, 2 * I, H), "w2": rnd(E, I // 8, H, 8),
-        })
-    return {"embed_tokens": rnd(c.vocab_size, H), "layers": layers, "norm": ones(H),
-            "lm_head": rnd(c.vocab_size, H)}
+    return {
+        "input_layernorm": ones(H), "post_attention_layernorm": ones(H),
+        "wqkv": rnd((nq + 2 * nkv) * D, H), "q_norm": ones(D), "k_norm": ones(D),
+        "wo": rnd(H, nq * D), "router": rnd(E, H),
+        "w13": rnd(E, 2 * I, H), "w2": rnd(E, I // 8, H, 8),
+    }
 
 
-def convert_qwen3_moe_hf_to_neuron_state_dict(state_dict: Dict[str, torch.Tensor],
-                                               config: Qwen3MoeInferenceConfig) -> Dict[str, Any]:
+def random_params(config: Qwen3MoeInferenceConfig, device, seed: int = 0, std: float = 0.02) -> Dict[str, Any]:
+    """Random-init bf16 weights of the model, generated on the GPU from ``seed``
+    (N(0, std) matrices; RMSNorm weights 1)."""
+    c = config
+    g = torch.Generator(device=device).manual_seed(seed)
+    H = c.hidden_size
+
+    def rnd(*shape):
+        return torch.empty(*shape, dtype=torch.bfloat16, device=device).normal_(0.0, std, generator=g)
+
+    layers = [random_layer_params(c, device, g, std) for _ in range(c.num_hidden_layers)]
+    return {"embed_tokens": rnd(c.vocab_size, H), "layers": layers,
+            "norm": torch.ones(H, dtype=torch.bfloat16, device=device), "lm_head": rnd(c.vocab_size, H)}
+
+
+def dequantize_fp8_block(weight: torch.Tensor, scale_inv: torch.Tensor, block_size,
+                         dtype=torch.bfloat16) -> torch.Tensor:
+    """Block-scaled fp8 weight -> ``dtype``: element ``(r, c)`` is
+    ``fp32(weight[r, c]) * scale_inv[r // b0, c // b1]`` with ``block_size =
+    (b0, b1)`` (``maybe_dequantize_layer``, qwen_with_nki.py:8865-8880; the
+    checkpoint's ``*_scale_inv`` tensors multiply).  A partial last block
+    uses its block's scale."""
+    if not block_size or len(block_size) != 2:
+        raise ValueError("fp8 weights need config.quantization_config['weight_block_size'] = [b0, b1]")
+    b0, b1 = int(block_size[0]), int(block_size[1])
+    if weight.dim() != 2 or scale_inv.dim() != 2:
+        raise ValueError("block dequantisation takes 2-D weights and scales")
+    R, C = weight.shape
+    if scale_inv.shape != (-(-R // b0), -(-C // b1)):
+        raise ValueError(f"scale_inv {tuple(scale_inv.shape)} does not tile a {R}x{C} weight in {b0}x{b1} blocks")
+    s = scale_inv.float().repeat_interleave(b0, dim=0).repeat_interleave(b1, dim=1)[:R, :C]
+    return (weight.float() * s).to(dtype)
+
+
+class SafetensorsDir(Mapping):
+    """Lazy ``key -> tensor`` view of the ``*.safetensors`` shards of a local
+    checkpoint directory: a tensor is read (memory-mapped) when it is asked
+    for, so a converter can go one layer at a time."""
+
+    def __init__(self, path: str):
+        from safetensors import safe_open
+
+        self._handles, self._where = {}, {}
+        for f in sorted(os.listdir(path)):
+            if f.endswith(".safetensors"):
+                h = safe_open(os.path.join(path, f), framework="pt", device="cpu")
+                self._handles[f] = h
+                for k in h.keys():
+                    self._where[k] = f
+        if not self._where:
+            raise ValueError(f"no *.safetensors tensors under {path}")
+
+    def __getitem__(self, key):
+        return self._handles[self._where[key]].get_tensor(key)
+
+    def __iter__(self):
+        return iter(self._where)
+
+    def __len__(self):
+        return len(self._where)
+
+
+def convert_qwen3_moe_hf_to_neuron_state_dict(state_dict, config: Qwen3MoeInferenceConfig,
+                                               device=None) -> Dict[str, Any]:
     """HF checkpoint tensors -> this build's parameter tree.
 
     Same key mapping as convert_qwen3_moe_hf_to_neuron_state_dict
-    (qwen_with_nki.py:8883-8997): q/k/v concatenated (8845-8862), q_norm/k_norm,
-    router from ``mlp.gate.weight`` (8915-8919), per-expert gate/up/down packed
-    (8928-8990) -- here into the gate/up-interleaved ``w13 [E,2I,H]`` and
-    blocked ``w2 [E,I/8,H,8]`` layouts.  Accepts keys with or without the ``model.`` prefix.
-    """
-    sd = {k[len("model."):] if k.startswith("model.") else k: v for k, v in state_dict.items()}
-    bf = lambda t: t.to(torch.bfloat16).contiguous()
+    (qwen_with_nki.py:8883-8997): fp8 block dequantisation of every weight
+    that has a ``*_scale_inv`` partner (8865-8880), q/k/v concatenated
+    (8845-8862), q_norm/k_norm, router from ``mlp.gate.weight`` (8915-8919),
+    per-expert gate/up/down packed (8928-8990) -- here into the
+    gate/up-interleaved ``w13 [E,2I,H]`` and blocked ``w2 [E,I/8,H,8]``
+    layouts.  lm_head from ``lm_head.weight``, or the embedding when
+    ``tie_word_embeddings``.  Keys may carry the ``model.`` prefix.
+
+    ``state_dict`` is any mapping (a dict, or a lazy :class:`SafetensorsDir`).
+    With ``device`` each converted tensor is moved there as soon as it is
+    built, so host memory holds about one layer at a time."""
+    keys = {(k[len("model."):] if k.startswith("model.") else k): k for k in state_dict.keys()}
+    qcfg = getattr(config, "quantization_config", None) or {}
+    block = qcfg.get("weight_block_size") if isinstance(qcfg, dict) else getattr(qcfg, "weight_block_size", None)
+
+    def get(name):
+        if name not in keys:
+            raise KeyError(f"checkpoint has no tensor {name!r}")
+        t = state_dict[keys[name]]
+        if name + "_scale_inv" in keys:
+            t = dequantize_fp8_block(t, state_dict[keys[name + "_scale_inv"]], block)
+        return t
+
+    def put(t):
+        t = t.to(torch.bfloat16).contiguous()
+        return t.to(device) if device is not None else t
+
     layers = []
+    E = config.num_experts
     for l in range(config.num_hidden_layers):
         p = f"layers.{l}."
-        E = config.num_experts
         w13, w2 = weights.from_hf_experts(
-            [sd[f"{p}mlp.experts.{e}.gate_proj.weight"].float() for e in range(E)],
-            [sd[f"{p}mlp.experts.{e}.up_proj.weight"].float() for e in range(E)],
-            [sd[f"{p}mlp.experts.{e}.down_proj.weight"].float() for e in range(E)],
+            [get(f"{p}mlp.experts.{e}.gate_proj.weight").float() for e in range(E)],
+            [get(f"{p}mlp.experts.{e}.up_proj.weight").float() for e in range(E)],
+            [get(f"{p}mlp.experts.{e}.down_proj.weight").float() for e in range(E)],
         )
         layers.append({
-            "input_layernorm": bf(sd[f"{p}input_layernorm.weight"]),
-            "post_attention_layernorm": bf(sd[f"{p}post_attention_layernorm.weight"]),
-            "wqkv": bf(torch.cat([sd[f"{p}self_attn.q_proj.weight"], sd[f"{p}self_attn.k_proj.weight"],
-                                  sd[f"{p}self_attn.v_proj.weight"]])),
-            "q_norm": bf(sd[f"{p}self_attn.q_norm.weight"]), "k_norm": bf(sd[f"{p}self_attn.k_norm.weight"]),
-            "wo": bf(sd[f"{p}self_attn.o_proj.weight"]), "router": bf(sd[f"{p}mlp.gate.weight"]),
-            "w13": bf(w13), "w2": bf(w2),
+            "input_layernorm": put(get(f"{p}input_layernorm.weight")),
+            "post_attention_layernorm": put(get(f"{p}post_attention_layernorm.weight")),
+            "wqkv": put(torch.cat([get(f"{p}self_attn.q_proj.weight"), get(f"{p}self_attn.k_proj.weight"),
+                                   get(f"{p}self_attn.v_proj.weight")])),
+            "q_norm": put(get(f"{p}self_attn.q_norm.weight")), "k_norm": put(get(f"{p}self_attn.k_norm.weight")),
+            "wo": put(get(f"{p}self_attn.o_proj.weight")), "router": put(get(f"{p}mlp.gate.weight")),
+            "w13": put(w13), "w2": put(w2),
         })
-    lm = sd.get("lm_head.weight", state_dict.get("lm_head.weight"))
-    if lm is None and getattr(config, "tie_word_embeddings", False):
-        lm = sd["embed_tokens.weight"]
-    return {"embed_tokens": bf(sd["embed_tokens.weight"]), "layers": layers, "norm": bf(sd["norm.weight"]),
-            "lm_head": bf(lm)}
+        del w13, w2
+    if "lm_head.weight" in keys:
+        lm = get("lm_head.weight")
+    elif getattr(config, "tie_word_embeddings", False):
+        lm = get("embed_tokens.weight")
+    else:
+        raise KeyError("checkpoint has no lm_head.weight and tie_word_embeddings is false")
+    return {"embed_tokens": put(get("embed_tokens.weight")), "layers": layers, "norm": put(get("norm.weight")),
+            "lm_head": put(lm)}
 
 
 # ============================================================================ causal LM
@@ -350,14 +532,7 @@ class NeuronQwen3MoeForCausalLM:
     def _load_params(self):
         path = self.model_path
         if path and os.path.isdir(path) and any(f.endswith(".safetensors") for f in os.listdir(path)):
-            from safetensors.torch import load_file
-
-            sd = {}
-            for f in sorted(os.listdir(path)):
-                if f.endswith(".safetensors"):
-                    sd.update(load_file(os.path.join(path, f), device="cpu"))
-            params = convert_qwen3_moe_hf_to_neuron_state_dict(sd, self.config)
-            return _to_device(params, self.device)
+            return convert_qwen3_moe_hf_to_neuron_state_dict(SafetensorsDir(path), self.config, device=self.device)
         return random_params(self.config, self.device, seed=self.neuron_config.seed)
 
     def reset(self):
@@ -365,24 +540,35 @@ class NeuronQwen3MoeForCausalLM:
         self.position = 0
 
     # -- forward ---------------------------------------------------------------
-    def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
+    def prefill(self, input_ids: torch.Tensor, lengths: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Context encoding of ``input_ids[B,S]`` at positions 0..S-1; returns
-        last-position logits ``[B, V]`` (fp32)."""
+        the logits ``[B, V]`` (fp32) of each row's last token: position S-1, or
+        ``lengths[b] - 1`` for right-padded rows (pad tokens sit after a row's
+        end, so causal attention keeps them out of its real positions)."""
         B, S = input_ids.shape
         dev = self.device
         pos = torch.arange(S, device=dev, dtype=torch.int32).repeat(B)
         h = self.model.hidden(input_ids.to(dev), pos, B, S, 0)
-        last = h.view(B, S, -1)[:, -1].contiguous()
+        if lengths is None:
+            last = h.view(B, S, -1)[:, -1].contiguous()
+        else:
+            rows = torch.arange(B, device=dev) * S + lengths.to(dev).long() - 1
+            last = h.index_select(0, rows).contiguous()
         self.position = S
         return self.model.logits(last)
 
-    def decode_step(self, token_ids: torch.Tensor) -> torch.Tensor:
-        """One token per sequence at the current position; returns ``[B, V]`` logits."""
+    def decode_step(self, token_ids: torch.Tensor, positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One token per sequence, at ``positions[b]`` (default: the current
+        position for every row); returns ``[B, V]`` logits."""
         B = token_ids.shape[0]
         dev = self.device
-        pos = torch.full((B,), self.position, device=dev, dtype=torch.int32)
-        h = self.model.hidden(token_ids.to(dev).view(B, 1), pos, B, 1, self.position)
-        self.position += 1
+        if positions is None:
+            pos = torch.full((B,), self.position, device=dev, dtype=torch.int32)
+            self.position += 1
+        else:
+            pos = positions.to(device=dev, dtype=torch.int32).contiguous()
+            self.position = int(pos.max()) + 1
+        h = self.model.hidden(token_ids.to(dev).view(B, 1), pos, B, 1, 0, ctx_len=pos + 1)
         return self.model.logits(h)
 
     def forward(self, input_ids: torch.Tensor, attention_mask=None, position_ids=None, **kw) -> CausalLMOutput:
@@ -393,27 +579,34 @@ class NeuronQwen3MoeForCausalLM:
     __call__ = forward
 
     # -- greedy decode with a captured step --------------------------------------
-    def greedy_decode(self, first_token: torch.Tensor, n_steps: int, use_graph: Optional[bool] = None) -> torch.Tensor:
-        """``n_steps`` greedy tokens after ``first_token[B]``; with a HIP graph
-        the whole step (embedding, 48 layers, lm_head, argmax, position += 1)
-        is one replay.  Returns ``[B, n_steps]`` token ids."""
+    def greedy_decode(self, first_token: torch.Tensor, n_steps: int, use_graph: Optional[bool] = None,
+                      positions: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``n_steps`` greedy tokens after ``first_token[B]``, row b starting at
+        ``positions[b]`` (default: the current position for every row); with a
+        HIP graph the whole step (embedding, 48 layers, lm_head, argmax,
+        position += 1) is one replay.  Returns ``[B, n_steps]`` token ids."""
         use_graph = self.neuron_config.use_hip_graphs if use_graph is None else use_graph
         B = first_token.shape[0]
+        if positions is None:
+            positions = torch.full((B,), self.position, dtype=torch.int32)
+        pos0 = positions.to(device=self.device, dtype=torch.int32).view(B)
+        top = int(pos0.max())
         if not use_graph:
             toks, cur = [], first_token.to(self.device)
-            for _ in range(n_steps):
-                cur = ops.argmax(self.decode_step(cur))
+            for i in range(n_steps):
+                cur = ops.argmax(self.decode_step(cur, pos0 + i))
                 toks.append(cur)
+            self.position = top + n_steps
             self.model.check_embed()
             return torch.stack(toks, dim=1)
         st = self._decode_state(B)
         st["tok"].copy_(first_token.to(self.device).view(B).long())
-        st["pos"].fill_(self.position)
+        st["pos"].copy_(pos0)
         out = torch.empty(B, n_steps, dtype=torch.long, device=self.device)
         for i in range(n_steps):
-            self._decode_graph(B, self._bucket(self.position + i + 1)).replay()
+            self._decode_graph(B, self._bucket(top + i + 1)).replay()
             out[:, i].copy_(st["tok"])
-        self.position += n_steps
+        self.position = top + n_steps
         self.model.check_embed()
         return out
 
@@ -575,16 +768,6 @@ class NeuronQwen3MoeForCausalLM:
 
 
 
-def _to_device(params, device):
-    if isinstance(params, torch.Tensor):
-        return params.to(device)
-    if isinstance(params, dict):
-        return {k: _to_device(v, device) for k, v in params.items()}
-    if isinstance(params, list):
-        return [_to_device(v, device) for v in params]
-    return params
-
-
 # ============================================================================ generation
 class HuggingFaceGenerationAdapter:
     """``generate`` for :class:`NeuronQwen3MoeForCausalLM` (main.py:503,
@@ -607,16 +790,32 @@ class HuggingFaceGenerationAdapter:
         if S + max_new_tokens > m.neuron_config.max_length + 1:
             raise ValueError(f"prompt + new tokens ({S}+{max_new_tokens}) exceed max_length "
                              f"{m.neuron_config.max_length}")
+        # right-padded prompts (main.py:366, 480-486): row b has lengths[b]
+        # real tokens; its new tokens continue from position lengths[b] and,
+        # as in HF generate, are appended after the padded prompt row
+        lengths = None
+        if attention_mask is not None:
+            _check_causal_mask(attention_mask, torch.zeros(B, 1, dtype=torch.int64))
+            am = attention_mask.detach().to("cpu", torch.int64)
+            if am.shape != (B, S):
+                raise ValueError(f"attention_mask must be [{B}, {S}] like input_ids")
+            lengths = am.sum(1)
+            if bool((lengths < 1).any()):
+                raise ValueError("every prompt row needs at least one real token")
+            if bool((lengths == S).all()):
+                lengths = None
         spec = int(getattr(m.neuron_config, "speculation_length", 0))
         if spec >= 2 and B == 1 and max_new_tokens > 1:
-            out, _ = m.spec_generate(input_ids, max_new_tokens, spec_len=spec)
-            return out.to(m.device)
+            prompt = input_ids if lengths is None else input_ids[:, : int(lengths[0])]
+            out, _ = m.spec_generate(prompt, max_new_tokens, spec_len=spec)
+            return torch.cat([input_ids.to(m.device), out[:, prompt.shape[1]:].to(m.device)], dim=1)
         m.reset()
-        logits = m.prefill(input_ids)
+        logits = m.prefill(input_ids, lengths)
         first = logits.argmax(dim=-1)
         if max_new_tokens <= 1:
             new = first.view(B, -1)[:, :max_new_tokens]
         else:
-            rest = m.greedy_decode(first, max_new_tokens - 1)
+            rest = m.greedy_decode(first, max_new_tokens - 1,
+                                   positions=None if lengths is None else lengths.to(torch.int32))
             new = torch.cat([first.view(B, 1), rest], dim=1)
         return torch.cat([input_ids.to(new.device), new], dim=1)

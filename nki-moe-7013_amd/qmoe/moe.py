@@ -14,6 +14,7 @@ Host-side mirror of the reference's MoE module surface:
 
 from __future__ import annotations
 
+from types import SimpleNamespace
 from typing import Optional
 
 import torch
@@ -39,6 +40,11 @@ class ExpertMLPs:
         self.intermediate_size = w13.shape[1] // 2
         self.top_k = top_k
         self.normalize_top_k_affinities = normalize_top_k_affinities
+        # NxDI's RoutedExpertsMLPOpsConfig flag the prefill seam reads
+        # (qwen_with_nki.py:5768): scale the input rows by the affinity before
+        # the MLP instead of the output after it.  Only the default (False,
+        # Qwen3's setting) is implemented; the seam rejects True.
+        self.routed_experts_mlp_config = SimpleNamespace(early_expert_affinity_modulation=False)
 
     def run(self, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
             residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -58,6 +64,9 @@ class ExpertMLPs:
         affinities from ``expert_affinities[T,E]``, L1-normalise them when
         ``normalize_top_k_affinities``, and return ``sum_j aff_j * mlp_j(x)``
         as ``[T,H]`` in the input dtype."""
+        if getattr(self.routed_experts_mlp_config, "early_expert_affinity_modulation", False):
+            raise ValueError("early_expert_affinity_modulation=True is not implemented (the reference "
+                             "routes it to the stock path, qwen_with_nki.py:3449)")
         T = hidden_states.shape[0]
         idx = expert_index.to(torch.int32).contiguous()
         chosen = torch.gather(expert_affinities.float(), 1, expert_index.long())
@@ -78,6 +87,10 @@ class ExpertMLPs:
         through the build's own permutation (a token never repeats within
         one expert, so the reference's duplicate redirection is not needed).
         """
+        if getattr(self.routed_experts_mlp_config, "early_expert_affinity_modulation", False):
+            raise ValueError("early_expert_affinity_modulation=True (affinity applied to the MLP input, "
+                             "qwen_with_nki.py:5768-5775) is not implemented: the experts here scale "
+                             "the MLP output by the affinity")
         T, H = hidden_states.shape
         E = self.num_experts
         tok = token_position_to_id.view(int(num_blocks), int(block_size)).long()

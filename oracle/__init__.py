@@ -28,5 +28,4 @@ from .qwen3_moe import (  # noqa: F401
     attention_layer,
     decoder_layer,
     pack_w13,
-    nxdi_to_hf_experts,
 )

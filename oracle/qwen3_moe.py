@@ -357,11 +357,6 @@ def decoder_layer(h, w: Dict[str, torch.Tensor], positions, cfg, past_kv=None):
 # ----------------------------------------------------------------------------
 # Layout helpers used by tests to hand the same weights to other implementations
 # ----------------------------------------------------------------------------
-def nxdi_to_hf_experts(gate_up: torch.Tensor, down: torch.Tensor):
-    """NxDI ``(E,H,2I)`` / ``(E,I,H)`` -> transformers-v5 ``(E,2I,H)`` / ``(E,H,I)``."""
-    return gate_up.transpose(1, 2).contiguous(), down.transpose(1, 2).contiguous()
-
-
 def pack_w13(gate_up: torch.Tensor, group: int = 32) -> torch.Tensor:
     """Reference re-layout used to check the product's packer.
 

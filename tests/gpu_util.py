@@ -46,3 +46,15 @@ def gap_mask(logits: torch.Tensor, k: int) -> torch.Tensor:
     """Rows whose k-th and (k+1)-th largest logits differ by more than GAP."""
     top = torch.topk(logits.float(), k + 1, dim=-1).values
     return (top[:, k - 1] - top[:, k]) > GAP
+
+
+def routing_agreement(y_ref: torch.Tensor, router: torch.Tensor, k: int, ours_idx: torch.Tensor):
+    """Rows where the product and the fp32 reference chose the same experts,
+    and the reference's k-th/(k+1)-th logit gap per row.  The product routes
+    from the bf16 normed hidden state (as the reference's bf16 pipeline does),
+    the reference from fp32, so near-tied rows may legitimately differ."""
+    logits = y_ref.float() @ router.float().t()
+    top = torch.topk(logits, k + 1, dim=-1)
+    gap = top.values[:, k - 1] - top.values[:, k]
+    same = (top.indices[:, :k].sort(-1).values == ours_idx.long().sort(-1).values).all(-1)
+    return same, gap

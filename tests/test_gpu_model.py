@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import announce, assert_close_layer
+from gpu_util import announce, assert_close_layer, routing_agreement
 from model_ref import ReferenceModel, cfg_dict, layer_weights_f32
 
 import qwen_with_nki as qn
@@ -32,18 +32,6 @@ def _config(n_layers, max_length, batch=1):
 def _fp32():
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
-
-
-def _routing_agreement(y_ref, router, k, ours_idx):
-    """Rows where the product and the fp32 reference chose the same experts,
-    and the reference's k-th/(k+1)-th logit gap per row.  The product routes
-    from the bf16 normed hidden state (as the reference's bf16 pipeline does),
-    the reference from fp32, so near-tied rows may legitimately differ."""
-    logits = y_ref.float() @ router.float().t()
-    top = torch.topk(logits, k + 1, dim=-1)
-    gap = top.values[:, k - 1] - top.values[:, k]
-    same = (top.indices[:, :k].sort(-1).values == ours_idx.long().sort(-1).values).all(-1)
-    return same, gap
 
 
 @pytest.mark.parametrize("B,S,steps", [(2, 40, 3), (1, 130, 2)])
@@ -73,7 +61,7 @@ def test_decoder_layer_prefill_then_decode(dev, B, S, steps):
                                       None if step == 0 else (past[0][:, :, :-1], past[1][:, :, :-1]))
         y = oracle.rmsnorm(x + a, w["post_attention_layernorm"], c["eps"]).reshape(B * n, -1)
         torch.cuda.synchronize()
-        same, gap = _routing_agreement(y, w["router"], c["top_k"], layer.mlp.last_routing[2])
+        same, gap = routing_agreement(y, w["router"], c["top_k"], layer.mlp.last_routing[2])
         # expert choices may differ only where the reference itself is near a tie
         assert bool(same[gap > 1e-2].all()), "routing differs on a row with a clear router-logit gap"
         assert same.float().mean() >= 0.9
