@@ -207,19 +207,88 @@ def bench_decode(layers, T, steps, warmup, dev):
     }
 
 
+def zipf_targets(n_experts, T, k, s=1.1):
+    """Rows per expert, by popularity rank r = 1..E, when expert popularity
+    follows Zipf(s) under top-k routing: n_r = min(T, C * r^-s) with C set so
+    that sum(n_r) = T * k.  An expert takes each token at most once, so the
+    head of the distribution saturates at T (water-filling).  Returns a list
+    of E floats, rank 1 first."""
+    w = [(r + 1) ** -s for r in range(n_experts)]
+    lo, hi = 0.0, float(T) * n_experts
+    for _ in range(200):
+        c = 0.5 * (lo + hi)
+        if sum(min(T, c * x) for x in w) > T * k:
+            hi = c
+        else:
+            lo = c
+    return [min(float(T), lo * x) for x in w]
+
+
+def zipf_router_bias(x, w_router, k, s=1.1, rank_seed=5, iters=400, step=0.3):
+    """A per-expert router bias under which the routing of the tokens ``x``
+    follows Zipf(s) popularity: experts get popularity ranks from a seeded
+    permutation and ``top-k(x . w_router^T + bias)`` takes expert e in about
+    ``zipf_targets(...)[rank(e) - 1]`` rows.  Fitted by damped log-count
+    updates on the tokens' own fp32 logits (selection counts rise
+    monotonically with an expert's bias); an expert whose target is every
+    token gets the least bias that puts it in each token's top-k.  Returns
+    ``(bias f32 [E] on x's device, target rows per expert id)``."""
+    import torch
+
+    T, n_e = x.shape[0], w_router.shape[0]
+    rank = torch.randperm(n_e, generator=torch.Generator().manual_seed(rank_seed))
+    tgt = torch.tensor(zipf_targets(n_e, T, k, s), dtype=torch.float32)[rank].to(x.device)
+    logits = x.float() @ w_router.float().t()
+    bias = torch.zeros(n_e, dtype=torch.float32, device=x.device)
+    sat = tgt >= T - 0.5  # experts every token must choose
+    n_sat = int(sat.sum())
+    for _ in range(iters):
+        if n_sat:
+            # the least bias that puts each saturated expert in every token's
+            # top-k: above the (k - n_sat + 1)-th largest other biased logit
+            other = (logits + bias).masked_fill(sat, float("-inf"))
+            v = torch.topk(other, k - n_sat + 1, dim=1).values[:, -1:]
+            bias[sat] = (v - logits[:, sat]).max(dim=0).values + 1e-3
+        idx = torch.topk(logits + bias, k, dim=1).indices
+        cnt = torch.bincount(idx.flatten(), minlength=n_e).float()
+        upd = step * (torch.log(tgt + 0.5) - torch.log(cnt + 0.5))
+        bias += upd.masked_fill(sat, 0.0)
+    return bias, tgt
+
+
+def routing_histogram(top_i, target, T):
+    """Achieved rows per expert against the Zipf target, for the bench line."""
+    import torch
+
+    cnt = torch.bincount(top_i.long().flatten(), minlength=target.numel()).float()
+    order = torch.argsort(target, descending=True)
+    return {
+        "zipf_s": 1.1,
+        "target_rows_top8": [round(float(v)) for v in target[order][:8]],
+        "achieved_rows_top8": [int(v) for v in cnt[order][:8]],
+        "target_rows_min": round(float(target.min())),
+        "achieved_rows_min": int(cnt.min()),
+        "experts_below_32_rows": int((cnt < 32).sum()),
+        "touched_experts": int((cnt > 0).sum()),
+        "l1_vs_target": float((cnt - target).abs().sum() / (T * K_TOP)),
+    }
+
+
 def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
-    """MoE block at prefill shape with Zipf(1.1)-skewed routing (router bias)."""
+    """MoE block at prefill shape with Zipf(1.1) expert popularity: a router
+    bias per layer fitted so that the 4096 tokens' top-8 routing follows the
+    Zipf(1.1) row targets (the most popular expert takes every token)."""
     import torch
 
     from qmoe import ops
     from qmoe.moe import MoEBlock, TILE_M
 
     g = torch.Generator(device=dev).manual_seed(77)
-    rank = torch.randperm(E, generator=torch.Generator().manual_seed(5)).float() + 1.0
-    bias = (-zipf_s * torch.log(rank)).to(dev)  # skewed expert popularity (Zipf-like)
     L = min(4, len(layers))
     xs = [torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
-    blocks = [MoEBlock(*layers[l], K_TOP, router_bias=bias) for l in range(L)]
+    fits = [zipf_router_bias(xs[l], layers[l][0], K_TOP, zipf_s) for l in range(L)]
+    biases = [f[0] for f in fits]
+    blocks = [MoEBlock(*layers[l], K_TOP, router_bias=biases[l]) for l in range(L)]
 
     def run():
         for l in range(L):
@@ -227,15 +296,14 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
 
     spread = [50]
     secs, ev_secs, done = time_graph(run, L, reps * L, 5 * L, spread=spread)
-    counts = []
+    counts, routes = [], []
     for l in range(L):
-        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
+        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, biases[l])
         counts.append(torch.bincount(ti.long().flatten(), minlength=E))
-    cnt = torch.stack(counts).float().mean(0)
-    routes = []
-    for l in range(L):
-        _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, bias)
         routes.append(ops.moe_permute(ti, E, TILE_M))
+        if l == 0:
+            hist = routing_histogram(ti, fits[0][1], T)
+    cnt = torch.stack(counts).float().mean(0)
 
     def run_experts(i):
         l = i % L
@@ -259,6 +327,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         "experts_TFLOPs": flops / (mean_ms * 1e-3) / 1e12,
         "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "top_expert_share": float(cnt.max() / cnt.sum()),
+        "routing_vs_zipf": hist,
     }
 
 

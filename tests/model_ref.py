@@ -71,13 +71,18 @@ class ReferenceModel:
                 rows.append(torch.sum(per_e * top_w[t].unsqueeze(1), dim=0))
             m = torch.stack(rows)
         top = torch.topk(logits, k + 1, dim=-1).values
-        self.min_gap = min(self.min_gap, float((top[:, k - 1] - top[:, k]).min()))
+        gap = top[:, k - 1] - top[:, k]
+        self.min_gap = min(self.min_gap, float(gap.min()))
+        self._gaps = gap if self._gaps is None else torch.minimum(self._gaps, gap)
         return h1 + m.view(B, S, H)
 
     def logits(self, input_ids, positions):
         h = torch.nn.functional.embedding(input_ids, self.p["embed_tokens"]).float()
+        self._gaps = None
         for i in range(len(self.p["layers"])):
             h = self._layer(i, h, positions)
+        self.last_hidden = h  # fp32 [B, S, H] after the last layer, before the final norm
+        self.last_gaps = self._gaps  # per token: smallest k-th/(k+1)-th router gap over the layers
         last = oracle.rmsnorm(h[:, -1], self.p["norm"].float(), self.cfg["eps"])
         return last @ self.p["lm_head"].float().t()
 
@@ -86,6 +91,7 @@ class ReferenceModel:
         dev = prompt.device
         pos = torch.arange(S, device=dev).expand(B, S)
         lg = self.logits(prompt, pos)
+        self.prompt_hidden, self.prompt_logits, self.prompt_gaps = self.last_hidden, lg, self.last_gaps
         toks, gaps = [lg.argmax(-1)], [_top2_gap(lg)]
         for t in range(1, n_new):
             p = torch.full((B, 1), S + t - 1, device=dev)

@@ -334,6 +334,53 @@ def test_moe_block_vs_oracle(dev, experts, router_w, T):
     assert_close_layer(out.cpu()[rows], ref, f"moe block T={T}")
 
 
+def test_moe_block_prefill_zipf_T4096(dev, experts, router_w):
+    """The prefill MoE block workload: T = 4096 tokens, H = 2048, 128 experts,
+    top-8, I = 768, with the router bias fitted so that expert popularity
+    follows Zipf(1.1) (the most popular expert takes every token: 16
+    consecutive 256-row tiles; the coldest about 40 rows).  Routing: logits
+    within 1e-4, expert ids exact wherever the gap exceeds 1e-3, histogram
+    within 2% L1 of the Zipf targets.  Output: 160 sampled rows (including
+    every row routed to the 8 coldest experts) vs oracle.moe_block_prefill."""
+    import bench
+
+    announce("moe block prefill T=4096, Zipf(1.1) routing")
+    w13, w2 = experts
+    T = 4096
+    g = torch.Generator(device=dev).manual_seed(4096)
+    x = bf16_randn((T, H), g, dev)
+    bias, target = bench.zipf_router_bias(x, router_w, K_TOP)
+    blk = MoEBlock(router_w, w13, w2, K_TOP, router_bias=bias)
+    residual = torch.randn(T, H, generator=g, device=dev)
+    out = blk(x, residual)
+    torch.cuda.synchronize()
+    logits, tw, ti = blk.last_routing
+    rl, rw, ri = oracle.router_topk(x.cpu(), router_w.cpu(), K_TOP, bias.cpu())
+    assert max_abs(logits, rl) <= 1e-4
+    ok = gap_mask(rl, K_TOP)
+    assert ok.float().mean() > 0.8
+    assert torch.equal(ti.cpu().long()[ok], ri[ok])
+    hist = bench.routing_histogram(ti, target, T)
+    print(f"  routing vs Zipf(1.1): {hist}", flush=True)
+    assert hist["achieved_rows_top8"][0] == T
+    assert hist["l1_vs_target"] < 0.02 and hist["experts_below_32_rows"] == 0
+    # sampled rows: every row of the 8 coldest experts, then random rows
+    cold = torch.argsort(target)[:8].cpu()
+    tic = ti.cpu().long()
+    cold_rows = torch.nonzero(torch.isin(tic, cold).any(1)).flatten()
+    cold_rows = cold_rows[ok[cold_rows]][:96]
+    rng = np.random.default_rng(3)
+    extra = torch.from_numpy(rng.choice(np.flatnonzero(ok.numpy()), 160 - len(cold_rows), replace=False))
+    rows = torch.unique(torch.cat([cold_rows, extra]))
+    gate_up = weights.unpack_gate_up(w13).float()  # (E, H, 2I), on the GPU
+    down = weights.unpack_down(w2).float()  # (E, I, H)
+    ref, r_i, _, _ = oracle.moe_block_prefill(x[rows.to(dev)], router_w, gate_up, down, K_TOP, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(r_i.cpu().sort(1).values, ri[rows].sort(1).values)
+    got = (out - residual)[rows.to(dev)]
+    assert_close_layer(got.cpu(), ref.cpu(), "moe block T=4096 Zipf(1.1)")
+
+
 def test_expert_seams_match_block(dev, experts, router_w):
     """forward_selective_loading / torch_blockwise_matmul_inference seams give
     the block's result for the same routing."""
@@ -433,6 +480,63 @@ def test_attn_prefill(dev, B, S, start):
                                kc.cpu()[:, :, : start + S], vc.cpu()[:, :, : start + S], qi)
     assert_close_layer(out.cpu().view(B, S, HQ, D), ref, f"attn_prefill B={B} S={S}",
                        max_abs_tol=2e-2, mean_rel_tol=5e-3)
+
+
+def test_attention_layer_B8_prefill1024_decode_to_8192(dev, attn_w):
+    """The attention-layer workload: batch 8, a 1024-token prefill into a
+    cache of 8193 rows, decode steps right after it (positions 1024, 1025),
+    then at context 1280 through the context-bucket launch (2048 rows) and at
+    context 8192 (the cache rows between hold other tokens' K/V, written
+    directly).  Each step through ``Attention.forward`` (QKV + q/k-norm +
+    RoPE + cache append, causal GQA, o_proj into the residual) vs the
+    oracle's attention layer over the same cache contents."""
+    from qmoe.attention import Attention, KVCache
+
+    announce("attention layer B=8 prefill 1024, decode at 1024, 1025, ctx 1280 and 8192")
+    wqkv, qn, kn = attn_w
+    B, S, S_max = 8, 1024, 8193
+    g = torch.Generator(device=dev).manual_seed(8192)
+    wo = bf16_randn((H, HQ * D), g, dev, std=0.02)
+    att = Attention(wqkv, qn, kn, wo, HQ, HKV, D, 1e-6)
+    cache = KVCache(B, HKV, S_max, D, dev)
+    cos, sin = _rope(S_max, dev)
+    wq, wk, wv = wqkv.float().split([HQ * D, HKV * D, HKV * D])
+    w = {"q_proj": wq, "k_proj": wk, "v_proj": wv, "o_proj": wo.float(), "q_norm": qn.float(),
+         "k_norm": kn.float()}
+    c = dict(n_q=HQ, n_kv=HKV, head_dim=D, eps=1e-6, theta=1.0e6)
+    # prefill
+    x = bf16_randn((B * S, H), g, dev)
+    pos = torch.arange(S, device=dev, dtype=torch.int32).repeat(B)
+    res = torch.zeros(B * S, H, device=dev)
+    att.forward(x, res, pos, B, S, cache, cos, sin, 0)
+    torch.cuda.synchronize()
+    ref, (rk, rv) = oracle.attention_layer(x.float().view(B, S, H), w, pos.view(B, S).long(), c)
+    rows = torch.from_numpy(np.random.default_rng(0).choice(B * S, 256, replace=False)).to(dev)
+    assert_close_layer(res[rows].cpu(), ref.reshape(B * S, H)[rows].cpu(), "attention prefill B=8 S=1024")
+    # cache rows: one bf16 rounding of the fp32 value, plus the difference of
+    # two fp32 summation orders over K = 2048 (the oracle's GEMM runs on the GPU here)
+    for what, a, r in (("k", cache.k[:, :, :S], rk), ("v", cache.v[:, :, :S], rv)):
+        err = (a.float() - r).abs() - r.abs() * 2 ** -8
+        assert float(err.max()) <= 1e-3, f"{what} cache rows after prefill"
+
+    def step(p, max_ctx=None, label=""):
+        xd = bf16_randn((B, H), g, dev)
+        pd = torch.full((B,), p, device=dev, dtype=torch.int32)
+        out = torch.zeros(B, H, device=dev)
+        past = (cache.k[:, :, :p].float().clone(), cache.v[:, :, :p].float().clone())
+        att.forward(xd, out, pd, B, 1, cache, cos, sin, 0, ctx_len=pd + 1, max_ctx=max_ctx)
+        torch.cuda.synchronize()
+        r, _ = oracle.attention_layer(xd.float().view(B, 1, H), w, pd.view(B, 1).long(), c, past)
+        assert_close_layer(out.cpu(), r.reshape(B, H).cpu(), f"attention decode {label}")
+
+    step(1024, label="position 1024")
+    step(1025, label="position 1025")
+    cache.k[:, :, 1026:1279] = bf16_randn((B, HKV, 253, D), g, dev)
+    cache.v[:, :, 1026:1279] = bf16_randn((B, HKV, 253, D), g, dev)
+    step(1279, max_ctx=2048, label="ctx 1280 (2048-row bucket)")
+    cache.k[:, :, 1280:8191] = bf16_randn((B, HKV, 6911, D), g, dev)
+    cache.v[:, :, 1280:8191] = bf16_randn((B, HKV, 6911, D), g, dev)
+    step(8191, label="ctx 8192")
 
 
 @pytest.mark.parametrize("K,N", [(512, 100), (2048, 5120), (4096, 2048)])

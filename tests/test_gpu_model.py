@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import announce, assert_close_layer, routing_agreement
+from gpu_util import announce, assert_close_layer, max_abs, mean_rel, routing_agreement
 from model_ref import ReferenceModel, cfg_dict, layer_weights_f32
 
 import qwen_with_nki as qn
@@ -108,6 +108,26 @@ def test_model_greedy_matches_fp32_reference(dev, n_layers, prompt_len, n_new):
     if match < n_new:
         print(f"  first divergence at step {match}: ours {got[0, match].item()} ref {ref_tok[0, match].item()}, "
               f"reference top-2 gap {gaps[match]:.5f}", flush=True)
+    # Depth accuracy: the prompt's final hidden states (after the last layer)
+    # and its last-position logits against the fp32 reference, over every
+    # token.  Each layer meets the layer bar (max-abs 2e-2, mean relative
+    # 5e-3); through the stack the bf16 intermediates' roundings add up, and a
+    # near-tied router decision may pick another expert for a token (the
+    # product routes from the bf16 normed state, the reference from fp32) and
+    # reach later tokens through attention.  The depth bar is therefore mean
+    # relative 2e-2 (measured: about 1e-2 at 4 and at 48 layers).
+    m.reset()
+    pos = torch.arange(prompt_len, device=dev, dtype=torch.int32)
+    h = m.model.hidden(prompt.to(dev), pos, 1, prompt_len, 0).clone()
+    lg = m.model.logits(h[-1:].contiguous())
+    torch.cuda.synchronize()
+    ref_h = ref.prompt_hidden.reshape(prompt_len, -1).cpu()
+    clear = (ref.prompt_gaps.reshape(-1) > 1e-2).cpu()
+    print(f"  {int(clear.sum())}/{prompt_len} tokens with a router gap > 1e-2 in every layer", flush=True)
+    assert_close_layer(h.cpu(), ref_h, f"final hidden states, {n_layers} layers", max_abs_tol=1.0,
+                       mean_rel_tol=2e-2)
+    assert_close_layer(lg.cpu(), ref.prompt_logits.cpu(), f"last-position logits, {n_layers} layers",
+                       max_abs_tol=0.2, mean_rel_tol=2e-2)
     if n_layers == 48:
         assert match == n_new  # the full workload: all 32 greedy tokens equal
     else:
