@@ -47,7 +47,7 @@ ROUTER_BYTES = E * H * 2
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=960)
+    ap.add_argument("--steps", type=int, default=960, help="timed MoE block calls (exactly this many)")
     ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--tokens", type=int, default=1, help="T tokens per MoE block call")
     ap.add_argument("--layers", type=int, default=48, help="distinct weight sets rotated through")
@@ -90,10 +90,14 @@ def make_layers(n_layers, dev, seed=0):
     return layers
 
 
-def time_graph(fn, steps_per_replay, steps, warmup, spread=None):
+def time_graph(fn, steps_per_replay, steps, warmup, spread=None, part=None):
     """Capture fn() (which performs steps_per_replay steps) in a HIP graph and
-    time ceil(steps / steps_per_replay) replays.  Returns (seconds by the host
-    clock, seconds by HIP events on the replay stream, steps_done).
+    time exactly ``steps`` steps: steps // steps_per_replay replays, then, when
+    ``part(r)`` is given (a function doing the first r steps), one replay of
+    a second graph capturing part(steps % steps_per_replay).  Without
+    ``part`` the step count is rounded up to whole replays.  ``warmup`` steps
+    run untimed first (whole replays).  Returns (seconds by the host clock,
+    seconds by HIP events on the replay stream, steps_done).
 
     With ``spread = n``, n further replays (after the timed region, not part
     of it) are each bracketed by their own HIP events, and the per-step
@@ -101,19 +105,27 @@ def time_graph(fn, steps_per_replay, steps, warmup, spread=None):
     the caller) for the median / p10 / p90."""
     import torch
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        fn()  # eager warm-up: allocations, lazy init
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        fn()
+    def capture(f):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            f()  # eager warm-up: allocations, lazy init
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            f()
+        return gr
+
+    graph = capture(fn)
+    rem = steps % steps_per_replay if part is not None else 0
+    tail = capture(lambda: part(rem)) if rem else None
     reps_w = max(1, math.ceil(warmup / steps_per_replay))
-    reps = max(1, math.ceil(steps / steps_per_replay))
+    reps = steps // steps_per_replay if part is not None else max(1, math.ceil(steps / steps_per_replay))
     for _ in range(reps_w):
         graph.replay()
+    if tail is not None:
+        tail.replay()
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -121,6 +133,8 @@ def time_graph(fn, steps_per_replay, steps, warmup, spread=None):
     ev0.record()
     for _ in range(reps):
         graph.replay()
+    if tail is not None:
+        tail.replay()
     ev1.record()
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
@@ -133,7 +147,7 @@ def time_graph(fn, steps_per_replay, steps, warmup, spread=None):
             b.record()
         torch.cuda.synchronize()
         spread.extend(a.elapsed_time(b) * 1e3 / steps_per_replay for a, b in evs)
-    return secs, ev0.elapsed_time(ev1) * 1e-3, reps * steps_per_replay
+    return secs, ev0.elapsed_time(ev1) * 1e-3, reps * steps_per_replay + rem
 
 
 def percentiles(us):
@@ -178,12 +192,13 @@ def bench_decode(layers, T, steps, warmup, dev):
     outs = [torch.empty(T, H, device=dev) for _ in range(L)]
     blocks = [MoEBlock(*w, K_TOP) for w in layers]
 
-    def all_layers():
-        for l in range(L):
+    def first_layers(n):
+        for l in range(n):
             blocks[l](xs[l], res[l], out=outs[l])
 
     spread = [60]  # 60 individually timed replays of the L-call graph
-    secs, ev_secs, done = time_graph(all_layers, L, steps, warmup, spread=spread)
+    secs, ev_secs, done = time_graph(lambda: first_layers(L), L, steps, warmup, spread=spread,
+                                     part=first_layers)
     U = []
     for l in range(L):
         _, _, ti = ops.router_topk(xs[l], layers[l][0], K_TOP)
@@ -275,18 +290,20 @@ def routing_histogram(top_i, target, T):
 
 
 def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
-    """MoE block at prefill shape with Zipf(1.1) expert popularity: a router
-    bias per layer fitted so that the 4096 tokens' top-8 routing follows the
-    Zipf(1.1) row targets (the most popular expert takes every token)."""
+    """MoE block at prefill shape.  With ``zipf_s``: Zipf(s) expert
+    popularity, a router bias per layer fitted so that the T tokens' top-8
+    routing follows the Zipf row targets (at T = 4096 the most popular expert
+    takes every token); without it the plain router (near-uniform load)."""
     import torch
 
     from qmoe import ops
     from qmoe.moe import MoEBlock, TILE_M
 
-    g = torch.Generator(device=dev).manual_seed(77)
+    g = torch.Generator(device=dev).manual_seed(77 + T)
     L = min(4, len(layers))
     xs = [torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16) for _ in range(L)]
-    fits = [zipf_router_bias(xs[l], layers[l][0], K_TOP, zipf_s) for l in range(L)]
+    fits = [zipf_router_bias(xs[l], layers[l][0], K_TOP, zipf_s) if zipf_s else (None, None)
+            for l in range(L)]
     biases = [f[0] for f in fits]
     blocks = [MoEBlock(*layers[l], K_TOP, router_bias=biases[l]) for l in range(L)]
 
@@ -296,12 +313,12 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
 
     spread = [50]
     secs, ev_secs, done = time_graph(run, L, reps * L, 5 * L, spread=spread)
-    counts, routes = [], []
+    counts, routes, hist = [], [], None
     for l in range(L):
         _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, biases[l])
         counts.append(torch.bincount(ti.long().flatten(), minlength=E))
         routes.append(ops.moe_permute(ti, E, TILE_M))
-        if l == 0:
+        if l == 0 and zipf_s:
             hist = routing_histogram(ti, fits[0][1], T)
     cnt = torch.stack(counts).float().mean(0)
 
@@ -328,6 +345,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "top_expert_share": float(cnt.max() / cnt.sum()),
         "routing_vs_zipf": hist,
+        "_cpu_case": (xs[0], biases[0]),  # layer 0's tokens and bias, for the CPU leg
     }
 
 
@@ -410,8 +428,13 @@ def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
         att.forward(x, res, pos, B, S, cache, cos, sin, 0)
 
     secs, ev_secs, done = time_graph(pre, 1, reps, 2)
+    # QKV + o_proj GEMMs and causal attention (S^2/2 scores, QK^T and PV)
     flops = 2 * B * S * Hd * (Hq + 2 * Hkv) * D + 2 * B * S * Hq * D * Hd + 2 * 2 * B * Hq * S * S // 2 * D
-    out = {"prefill_us": ev_secs / done * 1e6, "prefill_TFLOPs": flops / (ev_secs / done) / 1e12}
+    t_pre = ev_secs / done
+    out = {"prefill_us": t_pre * 1e6, "prefill_TFLOPs": flops / t_pre / 1e12,
+           "prefill_mfma_frac": flops / t_pre / 1e12 / BF16_PEAK_TFLOPS, "prefill_flop": flops,
+           "prefill_tokens_per_s": B * S / t_pre,
+           "_weights": (att.wqkv, att.q_norm, att.k_norm, att.wo)}
     xd = torch.randn(B, Hd, generator=g, device=dev).to(torch.bfloat16)
     rd = torch.zeros(B, Hd, device=dev)
     for L in ctx_points:
@@ -428,6 +451,9 @@ def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
             us = ev_secs / done * 1e6
             out[f"decode_ctx{L}{tag}_us"] = us
             out[f"decode_ctx{L}{tag}_GBps"] = byts / (us * 1e-6) / 1e9
+            out[f"decode_ctx{L}{tag}_hbm_frac"] = byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS
+            out[f"decode_ctx{L}{tag}_tokens_per_s"] = B / (us * 1e-6)
+        out[f"decode_ctx{L}_bytes"] = byts
     return out
 
 
@@ -478,16 +504,24 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     # part at a near-tied step (top-2 logits within ~1e-3 on this random model)
     same = (spec_out[0, prompt_len + 1:].cpu() == toks[0].cpu()).int()
     spec_prefix = int(same.cumprod(0).sum())
-    params_b = 61.06e9  # bytes of bf16 weights (30.53 B params)
+    # TTFT reads every weight but the embedding table (60.44 GB of bf16) and
+    # does 3.66 TFLOP (2 x 30.2 B non-embedding params x 640 tokens, and the
+    # causal attention): memory-bound at 7.56 ms for 8 TB/s
+    ttft_bytes, ttft_flop = 60.44e9, 3.66e12
     return {
         "ttft_ms": ttft_ms,
+        "ttft_hbm_frac": ttft_bytes / (ttft_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "ttft_mfma_frac": ttft_flop / (ttft_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "prefill_tokens_per_s": prompt_len / (ttft_ms * 1e-3),
         "decode_tokens_per_s": new_tokens / (dec_ms * 1e-3),
         "decode_ms_per_token": dec_ms / new_tokens,
         "decode_bytes_per_token_GB": 6.083,
         "decode_GBps": 6.083e9 / (dec_ms / new_tokens * 1e-3) / 1e9,
         "distinct_tokens": int(torch.unique(toks).numel()),
-        "spec_decode_tokens_per_s": new_tokens / (spec_ms * 1e-3),
+        # prompt-lookup speculation on this random-init model: its greedy
+        # stream repeats a few tokens, which n-gram lookup predicts almost
+        # always, so this is an upper bound on a repetitive sequence
+        "spec_decode_tokens_per_s_repetitive_upper_bound": new_tokens / (spec_ms * 1e-3),
         "spec_tokens_per_verify": (spec_stats["accepted"] + spec_stats["verify_steps"]) / max(1, spec_stats["verify_steps"]),
         "spec_steps": spec_stats["steps"],
         "spec_greedy_prefix_match": spec_prefix,
@@ -583,17 +617,70 @@ def measure_traffic(T):
     return res
 
 
-def cpu_baseline(layer, seconds, dev):
-    """fp32 CPU oracle (reference decode schedule, qwen_with_nki.py:3456-3478)
-    on one layer's weights: T=1 tokens with fresh random inputs until
-    ``seconds`` of work are done."""
+def cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on
+    (its affinity mask), capped by OMP_NUM_THREADS when that is set (a GPU
+    job's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_median(fn, warmup, runs, budget_s):
+    """Median seconds of fn() over up to ``runs`` timed calls after ``warmup``
+    untimed ones; stops early once ``budget_s`` of timed work is spent (at
+    least one timed call).  Returns (median seconds, calls timed)."""
+    for _ in range(warmup):
+        fn()
+    ts, t_all = [], time.perf_counter()
+    while len(ts) < runs and (not ts or time.perf_counter() - t_all < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def cpu_baseline(layer, attn_gpu, lm_head_gpu, prefill_case, dev, seconds):
+    """The fp32 CPU oracle (the reference's torch math restated) timed on the
+    host cores, one figure per GPU workload, weights copied from the GPU run:
+
+    * MoE block, decode schedule (qwen_with_nki.py:3456-3478) at T = 1, 8, 64;
+    * MoE block, prefill schedule (5728-5789) at T = 128 and at T = 4096 with
+      the GPU run's Zipf(1.1) router bias and tokens on the same layer
+      (``prefill_case = (x, bias)``: the same routing);
+    * the attention layer (10081-10109): B = 8 x 1024 prefill, one B = 8
+      decode step at context 1280 and at 8192;
+    * the model: one decoder layer (attention + MoE) at the model workload's
+      shapes times 48, plus the final norm and lm_head, for decode (T = 1 at
+      context 768) and for the 640-token prefill: an extrapolation.
+
+    ``seconds`` bounds the headline T = 1 sample; the others take a median of
+    up to 10 calls after warm-up, within a few seconds each."""
     import torch
 
     import oracle
     from qmoe import weights
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
+    t_start = time.perf_counter()
     w_router, w13, w2 = layer
     router = w_router.float().cpu()
     gate_up = torch.empty(E, H, 2 * I)
@@ -601,22 +688,81 @@ def cpu_baseline(layer, seconds, dev):
         gate_up[e0 : e0 + 16] = weights.unpack_gate_up(w13[e0 : e0 + 16]).float().cpu()
     down = weights.unpack_down(w2).float().cpu()  # (E, I, H)
     g = torch.Generator().manual_seed(0)
-    n = 0
-    for _ in range(3):  # warm-up
-        oracle.moe_block_decode(torch.randn(1, H, generator=g), router, gate_up, down, K_TOP)
-    t0 = time.perf_counter()
+    rnd = lambda *sh: torch.randn(*sh, generator=g)
+    out = {}
+
+    # headline: T = 1 decode MoE blocks, fresh tokens, until `seconds` elapse
+    for _ in range(3):
+        oracle.moe_block_decode(rnd(1, H), router, gate_up, down, K_TOP)
+    n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        x = torch.randn(1, H, generator=g).to(torch.bfloat16)
-        oracle.moe_block_decode(x, router, gate_up, down, K_TOP)
+        oracle.moe_block_decode(rnd(1, H).to(torch.bfloat16), router, gate_up, down, K_TOP)
         n += 1
     dt = time.perf_counter() - t0
+    out["moe_block_decode_T1"] = {"tokens_per_s": n / dt, "sample": f"{n} blocks in {dt:.1f} s"}
+    for T in (8, 64):
+        x = rnd(T, H)
+        sec, k = cpu_median(lambda: oracle.moe_block_decode(x, router, gate_up, down, K_TOP), 2, 10, 4.0)
+        out[f"moe_block_decode_T{T}"] = {"tokens_per_s": T / sec, "sample": f"median of {k} blocks"}
+    x = rnd(128, H)
+    sec, k = cpu_median(lambda: oracle.moe_block_prefill(x, router, gate_up, down, K_TOP), 2, 10, 4.0)
+    out["moe_block_prefill_T128"] = {"tokens_per_s": 128 / sec, "sample": f"median of {k} blocks"}
+    if prefill_case is not None:  # (tokens, Zipf bias) of the GPU run on this same layer
+        xz, bz = prefill_case[0].float().cpu(), prefill_case[1].float().cpu()
+        sec, k = cpu_median(lambda: oracle.moe_block_prefill(xz, router, gate_up, down, K_TOP, bz), 1, 5, 6.0)
+        out["moe_block_prefill_T4096_zipf"] = {"tokens_per_s": 4096 / sec, "sample": f"median of {k} blocks"}
+
+    # attention layer (B = 8), the GPU run's weights
+    Hq, Hkv, D = 32, 4, 128
+    wqkv, qn, kn, wo = (t.float().cpu() for t in attn_gpu)
+    wq, wk, wv = wqkv.split([Hq * D, Hkv * D, Hkv * D])
+    wa = {"q_proj": wq, "k_proj": wk, "v_proj": wv, "o_proj": wo, "q_norm": qn, "k_norm": kn}
+    c = dict(n_q=Hq, n_kv=Hkv, head_dim=D, eps=1e-6, theta=1.0e6)
+    xa = rnd(8, 1024, H)
+    pa = torch.arange(1024).expand(8, 1024)
+    sec, k = cpu_median(lambda: oracle.attention_layer(xa, wa, pa, c), 1, 3, 6.0)
+    out["attention_B8_prefill1024"] = {"tokens_per_s": 8 * 1024 / sec, "sample": f"median of {k} layers"}
+    del xa
+    for L in (1280, 8192):
+        past = (rnd(8, Hkv, L - 1, D), rnd(8, Hkv, L - 1, D))
+        xd, pd = rnd(8, 1, H), torch.full((8, 1), L - 1)
+        sec, k = cpu_median(lambda: oracle.attention_layer(xd, wa, pd, c, past), 2, 10, 4.0)
+        out[f"attention_B8_decode_ctx{L}"] = {"tokens_per_s": 8 / sec, "sample": f"median of {k} steps"}
+        del past
+
+    # the model: one decoder layer x 48 + final norm + lm_head (extrapolated)
+    wl = dict(wa, input_layernorm=torch.ones(H), post_attention_layernorm=torch.ones(H), router=router,
+              gate_up_proj=gate_up, down_proj=down)
+    cl = dict(c, top_k=K_TOP)
+    lm = lm_head_gpu.float().cpu()
+    norm_w = torch.ones(H)
+    head = lambda h: oracle.rmsnorm(h, norm_w, 1e-6) @ lm.t()
+    past = (rnd(1, Hkv, 767, D), rnd(1, Hkv, 767, D))
+    xd, pd = rnd(1, 1, H), torch.full((1, 1), 767)
+    sec_l, k = cpu_median(lambda: oracle.decoder_layer(xd, wl, pd, cl, past), 2, 10, 4.0)
+    sec_h, _ = cpu_median(lambda: head(xd[:, 0]), 1, 5, 2.0)
+    out["model_decode"] = {"tokens_per_s": 1.0 / (48 * sec_l + sec_h), "extrapolation": True,
+                           "sample": f"one decoder layer at T=1, context 768 (median of {k}) x 48 + lm_head"}
+    xp, pp = rnd(1, 640, H), torch.arange(640).view(1, 640)
+    sec_l, k = cpu_median(lambda: oracle.decoder_layer(xp, wl, pp, cl), 1, 3, 6.0)
+    ttft = 48 * sec_l + sec_h
+    out["model_prefill_640"] = {"tokens_per_s": 640 / ttft, "ttft_ms": ttft * 1e3, "extrapolation": True,
+                                "sample": f"one decoder layer at T=640 (median of {k}) x 48 + lm_head"}
+    head_line = out["moe_block_decode_T1"]
     return {
-        "value": n / dt,
+        "value": head_line["tokens_per_s"],
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} single-token MoE blocks (T=1, fp32, one layer's 128 experts), {dt:.1f} s",
-        "cpu": platform.processor() or platform.machine(),
+        "sample": (f"{head_line['sample']}: single-token MoE blocks (T=1, fp32, one layer's 128 experts, "
+                   "decode schedule of qwen_with_nki.py:3456-3478)"),
+        "cpu": cpu_model_name(),
+        "host_cpu_count": os.cpu_count(),
+        "threads": threads,
+        "torch": torch.__version__,
+        "dtype": "f32",
+        "workloads": out,
+        "secs": round(time.perf_counter() - t_start, 1),
     }
 
 
@@ -662,15 +808,20 @@ def main():
 
     dec = bench_decode(layers, a.tokens, a.steps, a.warmup, dev)
     print(f"[bench] decode T={a.tokens}: {dec}", file=sys.stderr, flush=True)
-    extra = {}
+    extra, prefill_case, attn_weights = {}, None, None
     if not a.no_prefill:
         extra["prefill_T4096"] = bench_prefill(layers, dev)
+        prefill_case = extra["prefill_T4096"].pop("_cpu_case")
         print(f"[bench] prefill: {extra['prefill_T4096']}", file=sys.stderr, flush=True)
+        extra["prefill_T128"] = bench_prefill(layers, dev, T=128, reps=50, zipf_s=None)
+        extra["prefill_T128"].pop("_cpu_case")
+        print(f"[bench] prefill T=128: {extra['prefill_T128']}", file=sys.stderr, flush=True)
     if not a.no_extra:
         for T in (8, 64):
             extra[f"decode_T{T}"] = bench_decode(layers, T, 480, 48, dev)
             print(f"[bench] decode T={T}: {extra[f'decode_T{T}']}", file=sys.stderr, flush=True)
         extra["attention_B8"] = bench_attention(dev)
+        attn_weights = extra["attention_B8"].pop("_weights")
         print(f"[bench] attention: {extra['attention_B8']}", file=sys.stderr, flush=True)
     if not a.no_model:
         extra["model_48L"] = model_child()
@@ -678,16 +829,67 @@ def main():
 
     peaks = measure_peaks(dev)
     print(f"[bench] measured peaks: {peaks}", file=sys.stderr, flush=True)
-    if "prefill_T4096" in extra:
-        extra["prefill_T4096"]["experts_frac_of_measured_mfma"] = (
-            extra["prefill_T4096"]["experts_TFLOPs"] / peaks["mfma_bf16_random_TFLOPs"])
+    for key in ("prefill_T4096", "prefill_T128"):
+        if key in extra:
+            extra[key]["experts_frac_of_measured_mfma"] = extra[key]["experts_TFLOPs"] / peaks["mfma_bf16_random_TFLOPs"]
 
     cpu = None
     if not a.no_cpu_baseline:
-        cpu = cpu_baseline(layers[0], a.cpu_seconds, dev)
+        if attn_weights is None:  # the attention leg was skipped: same shapes, fresh weights
+            gw = torch.Generator(device=dev).manual_seed(4)
+            mk = lambda *sh: torch.empty(*sh, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gw)
+            one = torch.ones(128, dtype=torch.bfloat16, device=dev)
+            attn_weights = (mk(48 * 128, H), one, one, mk(H, 32 * 128))
+        lm_head = torch.empty(151936, H, dtype=torch.bfloat16, device=dev).normal_(
+            0.0, 0.02, generator=torch.Generator(device=dev).manual_seed(6))
+        cpu = cpu_baseline(layers[0], attn_weights, lm_head, prefill_case, dev, a.cpu_seconds)
+        del lm_head
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
 
+    # every throughput with its roofline fraction and, beside it, the CPU
+    # oracle's figure for the same workload (cpu_baseline.workloads)
+    cw = (cpu or {}).get("workloads", {})
+    cpu_of = lambda k: round(cw[k]["tokens_per_s"], 2) if k in cw else None
+    tp = {"moe_block_decode_T1": {
+        "tokens_per_s": round(dec["tokens_per_s"], 1), "bound": "hbm", "hbm_frac": round(dec["block_frac"], 4),
+        "cpu_tokens_per_s": cpu_of("moe_block_decode_T1")}}
+    for T in (8, 64):
+        d = extra.get(f"decode_T{T}")
+        if d:
+            tp[f"moe_block_decode_T{T}"] = {"tokens_per_s": round(d["tokens_per_s"], 1), "bound": "hbm",
+                                            "hbm_frac": round(d["block_frac"], 4),
+                                            "cpu_tokens_per_s": cpu_of(f"moe_block_decode_T{T}")}
+    for key, name in (("prefill_T128", "moe_block_prefill_T128"), ("prefill_T4096", "moe_block_prefill_T4096_zipf")):
+        d = extra.get(key)
+        if d:
+            flop = d["T"] * K_TOP * 2 * 3 * H * I
+            bound = "mfma" if flop / (BF16_PEAK_TFLOPS * 1e12) > d["block_bytes"] / (HBM_PEAK_GBS * 1e9) else "hbm"
+            tp[name] = {"tokens_per_s": round(d["tokens_per_s"], 1), "bound": bound,
+                        "experts_mfma_frac": round(d["experts_mfma_frac"], 4),
+                        "experts_frac_of_measured_mfma": round(d["experts_frac_of_measured_mfma"], 4),
+                        "block_hbm_frac": round(d["block_hbm_frac"], 4), "cpu_tokens_per_s": cpu_of(name)}
+    at = extra.get("attention_B8")
+    if at:
+        tp["attention_B8_prefill1024"] = {"tokens_per_s": round(at["prefill_tokens_per_s"], 1), "bound": "mfma",
+                                          "mfma_frac": round(at["prefill_mfma_frac"], 4),
+                                          "cpu_tokens_per_s": cpu_of("attention_B8_prefill1024")}
+        for L in (1280, 8192):
+            tp[f"attention_B8_decode_ctx{L}"] = {
+                "tokens_per_s": round(at[f"decode_ctx{L}_tokens_per_s"], 1), "bound": "hbm",
+                "hbm_frac": round(at[f"decode_ctx{L}_hbm_frac"], 4),
+                "cpu_tokens_per_s": cpu_of(f"attention_B8_decode_ctx{L}")}
+    md = extra.get("model_48L", {})
+    if "decode_tokens_per_s" in md:
+        tp["model_decode"] = {"tokens_per_s": round(md["decode_tokens_per_s"], 2), "bound": "hbm",
+                              "hbm_frac": round(md["decode_GBps"] / HBM_PEAK_GBS, 4),
+                              "cpu_tokens_per_s": cpu_of("model_decode"), "cpu_extrapolated": True}
+        tp["model_prefill_640"] = {"tokens_per_s": round(md["prefill_tokens_per_s"], 1), "bound": "hbm",
+                                   "ttft_ms": round(md["ttft_ms"], 3), "hbm_frac": round(md["ttft_hbm_frac"], 4),
+                                   "mfma_frac": round(md["ttft_mfma_frac"], 4),
+                                   "cpu_tokens_per_s": cpu_of("model_prefill_640"), "cpu_extrapolated": True}
+
     achieved = dec["block_GBps"]
+    pre = extra.get("prefill_T4096", {})
     line = {
         "metric": METRIC,
         "value": round(dec["tokens_per_s"], 2),
@@ -711,26 +913,15 @@ def main():
         "moe_block_GBps": round(dec["block_GBps"], 1),
         "moe_block_hbm_frac": round(dec["block_frac"], 4),
         "moe_block_us_spread": dec["us_per_block_spread"],
-        # the companion workloads: prefill MoE block (T=4096, Zipf-skewed
-        # routing) and the full 48-layer model at batch 1 (child process)
-        "prefill_moe_block_tokens_per_s": (round(extra["prefill_T4096"]["tokens_per_s"], 1)
-                                           if "prefill_T4096" in extra else None),
-        "prefill_experts_mfma_frac": (round(extra["prefill_T4096"]["experts_mfma_frac"], 4)
-                                      if "prefill_T4096" in extra else None),
-        "prefill_block_hbm_frac": (round(extra["prefill_T4096"]["block_hbm_frac"], 4)
-                                   if "prefill_T4096" in extra else None),
-        "prefill_experts_frac_of_measured_mfma": (
-            round(extra["prefill_T4096"]["experts_frac_of_measured_mfma"], 4) if "prefill_T4096" in extra else None),
-        "model_decode_tokens_per_s": (round(extra["model_48L"]["decode_tokens_per_s"], 2)
-                                      if "decode_tokens_per_s" in extra.get("model_48L", {}) else None),
-        "model_decode_hbm_frac": (round(extra["model_48L"]["decode_GBps"] / HBM_PEAK_GBS, 4)
-                                  if "decode_GBps" in extra.get("model_48L", {}) else None),
-        "model_ttft_ms": (round(extra["model_48L"]["ttft_ms"], 3)
-                          if "ttft_ms" in extra.get("model_48L", {}) else None),
-        "model_prefill_tokens_per_s": (round(extra["model_48L"]["prefill_tokens_per_s"], 1)
-                                       if "prefill_tokens_per_s" in extra.get("model_48L", {}) else None),
-        "model_spec_decode_tokens_per_s": (round(extra["model_48L"]["spec_decode_tokens_per_s"], 1)
-                                           if "spec_decode_tokens_per_s" in extra.get("model_48L", {}) else None),
+        "prefill_moe_block_tokens_per_s": round(pre["tokens_per_s"], 1) if pre else None,
+        "prefill_experts_mfma_frac": round(pre["experts_mfma_frac"], 4) if pre else None,
+        "prefill_block_hbm_frac": round(pre["block_hbm_frac"], 4) if pre else None,
+        "prefill_experts_frac_of_measured_mfma": round(pre["experts_frac_of_measured_mfma"], 4) if pre else None,
+        "model_decode_tokens_per_s": round(md["decode_tokens_per_s"], 2) if "decode_tokens_per_s" in md else None,
+        "model_decode_hbm_frac": round(md["decode_GBps"] / HBM_PEAK_GBS, 4) if "decode_GBps" in md else None,
+        "model_ttft_ms": round(md["ttft_ms"], 3) if "ttft_ms" in md else None,
+        "model_prefill_tokens_per_s": round(md["prefill_tokens_per_s"], 1) if "prefill_tokens_per_s" in md else None,
+        "throughputs": tp,
         "roofline": {
             "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
                        "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else
