@@ -37,6 +37,8 @@
 // of 4 consecutive A rows.
 #pragma once
 
+#include <type_traits>
+
 #include "mfma_pipe.hpp"
 
 namespace qmoe {
@@ -130,30 +132,48 @@ struct Wide {
       wait_vm<0>();
     __syncthreads();
     if (NB > 0) load(0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const bool more = kt + S - 1 < nk;
+    // One stage.  MORE: stage kt+S-1 exists and is DMA'd during this one.
+    // LAST: no stage follows (no barrier, no next-stage reads).  The three
+    // variants are separate straight-line bodies (steady state, drain, last
+    // stage): with one body and runtime flags the compiler's wait-count
+    // analysis merges the paths and waits on the next stage's fragment reads
+    // before the MFMAs of this stage's last k-step, which use fragments
+    // loaded long before.
+    auto stage = [&](int kt, auto more_c, auto last_c) {
+      constexpr bool MORE = decltype(more_c)::value, LAST = decltype(last_c)::value;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         if (s + 1 < KS) {
           if (NB > 0) load(kt, s + 1, (s + 1) & 1);
-        } else if (kt + 1 < nk) {
+        } else if (!LAST) {
           // stage kt+1 landed: the DMAs issued after it are the full stages
           // kt+2..kt+S-2 and the first KS-1 parts of stage kt+S-1
-          if (more)
+          if (MORE)
             wait_vm<NDMA * (S - 3) + (KS - 1) * NDMA / KS>();
           else
             wait_vm<0>();
           __syncthreads();
           if (NB > 0) load(kt + 1, 0, 0);
         }
-        if (more) dma_part(kt + S - 1, s);
+        if (MORE) dma_part(kt + S - 1, s);
+        // keep the next k-step's fragment reads (and the DMAs) ahead of this
+        // k-step's MFMAs: left alone, the scheduler sinks the reads below the
+        // MFMAs, reuses the registers and every k-step waits on LDS latency
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    int kt = 0;
+    for (; kt < nk - (S - 1); ++kt) stage(kt, T_{}, F_{});
+    for (; kt < nk - 1; ++kt) stage(kt, F_{}, F_{});
+    if (kt < nk) stage(kt, F_{}, T_{});
   }
 
   // run<NB> for a runtime block count nb in [0, FN].
