@@ -265,6 +265,7 @@ constexpr int AP_QT = 128;      // query rows per workgroup (4 waves x 32)
 constexpr int AP_KT = 64;       // keys per step
 constexpr int AP_LDK = HD + 8;  // K tile row stride (bf16)
 constexpr int AP_LDV = AP_KT + 8;
+constexpr float AP_TAU = 8.0f;  // lazy-max slack (log2 units): p < 2^8 between rescales
 
 // position of key r (0..63) inside the permuted, transposed V tile row
 __device__ __forceinline__ int vt_slot(int key) {
@@ -308,10 +309,20 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  // Running max m_run (log2 units, shared by lanes l and l ^ 32, which hold
+  // the same query) and this lane's share of the row sum l_run.  The max is
+  // updated lazily: O and l are rescaled only when a query's tile max exceeds
+  // m_run by more than AP_TAU, so p = 2^(s - m_run) stays below 2^AP_TAU
+  // and most steps skip the rescale (O / l does not depend on which
+  // reference max was used).
   float m_run = -INFINITY, l_run = 0.0f;
   const int q_idx = start + qrow;               // cache index of this query
   const int kv_end = start + min(q0 + AP_QT, S);  // keys [0, kv_end) can be visible
   const int n_kt = (kv_end + AP_KT - 1) / AP_KT;
+  // keys this wave can see: [0, wave_last]; a tile that ends at or below
+  // wave_first is visible to every query of the wave (no mask)
+  const int wave_first = start + q0 + wave * 32;
+  const int wave_last = min(wave_first + 31, kv_end - 1);
 
   // One K/V tile per step, prefetched into registers during the previous
   // step's MFMAs.  K: chunk c = t + 256 j (key c / 16, dims (c % 16) * 8).
@@ -365,12 +376,16 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     lstore();
     if (kt + 1 < n_kt) gload(kt + 1);
     __syncthreads();
-    // S^T blocks: keys [0,32) and [32,64) x this wave's 32 queries
+    if (kv0 > wave_last) continue;  // past this wave's queries (wave-uniform)
+    // S^T blocks: keys [0,32) and [32,64) x this wave's 32 queries; a block
+    // wholly past the wave's last query is skipped (its scores are -inf)
+    const bool live1 = kv0 + 32 <= wave_last;
     f32x16 st[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
+      if (kb == 1 && !live1) break;
       const uint16_t* kp = Ks + (kb * 32 + (lane & 31)) * AP_LDK + hl * 8;
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
@@ -378,40 +393,52 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], st[kb], 0, 0, 0);
       }
     }
-    // scale (log2 domain), causal mask, online softmax
-    float mloc = -INFINITY;
+    // causal / range mask only where a tile reaches past the wave's first query
+    if (kv0 + AP_KT - 1 > wave_first || kv0 + AP_KT > kv_end) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kv0 + kb * 32 + (i >> 2) * 8 + hl * 4 + (i & 3);
+          if (key > q_idx || key >= kv_end) st[kb][i] = -INFINITY;
+        }
+    } else if (!live1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[1][i] = -INFINITY;
+    }
+    float mloc = fmaxf(st[0][0], st[0][1]);
+#pragma unroll
+    for (int i = 2; i < 16; ++i) mloc = fmaxf(mloc, st[0][i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, st[1][i]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
+    const bool grow = mloc > m_run + AP_TAU;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mloc : m_run;
+      // 1 where the max stays; 0 on a query's first visible tile (O, l are 0)
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      m_run = m_new;
+    }
+    // p = 2^(s * scale - m) in one FMA + v_exp (masked s = -inf gives 0); a
+    // lane with no visible key yet keeps m_run = -inf and every s = -inf
+    const float mb = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int key = kv0 + kb * 32 + (i >> 2) * 8 + hl * 4 + (i & 3);
-        float s = st[kb][i] * scale_log2;
-        if (key > q_idx || key >= kv_end) s = -INFINITY;
-        st[kb][i] = s;
-        mloc = fmaxf(mloc, s);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m_run - m_new);
-    float lsum = 0.0f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = (m_new == -INFINITY) ? 0.0f : exp2f(st[kb][i] - m_new);
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[kb][i], scale_log2, -mb));
         st[kb][i] = p;
-        lsum += p;
+        l_run += p;
       }
-    lsum += __shfl_xor(lsum, 32, 64);
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-    // O^T += V^T P^T over 4 steps of 16 keys
+    // O^T += V^T P^T over 4 steps of 16 keys (the last two only for live keys 32..63)
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      if (s >= 2 && !live1) break;
       bf16x8 pb;
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) pb[jj] = static_cast<__bf16>(st[s >> 1][(s & 1) * 8 + jj]);
@@ -423,6 +450,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
       }
     }
   }
+  l_run += __shfl_xor(l_run, 32, 64);
   if (qrow >= S) return;
   const float inv = 1.0f / l_run;
   uint16_t* op = out + ((int64_t(b) * S + qrow) * Hq + h) * HD;
