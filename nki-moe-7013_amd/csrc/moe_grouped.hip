@@ -5,7 +5,7 @@
 // (row tile, 256-row weight panel) pair on the direct-to-LDS pipeline of
 // mfma_wide.hpp (512 threads; A = 256 weight rows, B = up to 256 tokens; one
 // workgroup per CU).  Two pipelines share the grid, chosen per tile:
-//   - more than 64 live rows: 256 x 256 x 32 stages, three deep, only the
+//   - more than 64 live rows: 256 x 256 x 32 stages, four deep, only the
 //     live 32-row token blocks computed;
 //   - at most 64 live rows (cold experts, where streaming the weights is the
 //     whole cost): 256 x 64 x 64 stages, four deep, so three 32 KB weight
@@ -33,9 +33,10 @@
 namespace qmoe {
 
 namespace {
-// Full and partial tiles (more than 64 live rows): 256 x 256 x 32, three
-// stages, 8 waves (2 per SIMD) of 64 x 128.
-using Hot = pipe::Wide<4, 2, 32, 3, 256>;
+// Full and partial tiles (more than 64 live rows): 256 x 256 x 32, four
+// stages (three 32 KB stages in flight: a tile's weights are usually
+// streamed from HBM), 8 waves (2 per SIMD) of 64 x 128.
+using Hot = pipe::Wide<4, 2, 32, 4, 256>;
 // Cold tiles (at most 64 live rows: weight streaming dominates): 256 x 64 x 64,
 // four stages, so three 32 KB weight slabs are in flight and a barrier covers
 // 64 columns of K.
