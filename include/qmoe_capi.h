@@ -240,6 +240,25 @@ int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slo
 int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
               int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream);
 
+/* qmoe_gemm with a caller-owned workspace for split-K: when the problem has
+ * too few output tiles to occupy the GPU (prefill-size o_proj, 640 x 2048
+ * with K = 4096; the router logits, 640 x 128 with K = 2048), K is split into
+ * slices whose fp32 partial tiles go to `workspace` and a second launch adds
+ * them in slice order and applies `mode` (deterministic: no atomics).  Other
+ * problems, or a workspace smaller than qmoe_gemm_ws_workspace(M, N, K)
+ * bytes, take the qmoe_gemm path.  Same arguments and limits as qmoe_gemm.
+ * Calls sharing a workspace must not overlap.
+ * Replaces: the same projections as qmoe_gemm (o_proj qwen_with_nki.py:10089-
+ *   10099; router linear 8589-8590) at prefill sizes. */
+int qmoe_gemm_ws(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+                 int64_t K, int mode, void* C, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                 qmoe_stream_t stream);
+
+/* Workspace bytes qmoe_gemm_ws uses for an M x N x K problem (0: it does not
+ * split K for this shape); -1 for negative sizes.
+ * Replaces: nothing in the reference (caller-owned scratch). */
+int64_t qmoe_gemm_ws_workspace(int64_t M, int64_t N, int64_t K);
+
 /* One-row GEMV with the input RMSNorm fused into its activation staging:
  *   C[n] (mode as qmoe_gemm) = bf16(rms_w * h * rsqrt(mean(h^2) + eps)) . B[n]^T
  *   h: f32 [K] (the residual stream row); rms_w: bf16 [K]; B: bf16 [N, K].

@@ -197,8 +197,8 @@ struct QkvPipe {
   static_assert(SMEM <= 160 * 1024, "LDS");
 };
 
-template <class P>
-__global__ __launch_bounds__(256, 1) void qkv_pipe_kernel(
+template <class P, int OCC>
+__global__ __launch_bounds__(256, OCC) void qkv_pipe_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wqkv,
     const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
@@ -236,25 +236,25 @@ __global__ __launch_bounds__(256, 1) void qkv_pipe_kernel(
   __syncthreads();
   for (int r0 = 0; r0 < P::BM; r0 += 128) {
     const int row = r0 + (t >> 1), tok = m0 + row;
-    if (tok < T)
+    if (row < P::BM && tok < T)
       qkv_finish_head(ct + row * LDC, t & 1, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
                       kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
   }
 }
 
-template <class P>
+template <class P, int OCC>
 static int qkv_pipe_launch(const uint16_t* x, const uint16_t* wqkv, const uint16_t* qn_w, const uint16_t* kn_w,
                            const float* rope_cos, const float* rope_sin, const int32_t* positions, int64_t T,
                            int64_t S, int64_t H, int64_t Hq, int64_t Hkv, int64_t S_max, int max_p, float eps,
                            uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
   static const bool attr = [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_pipe_kernel<P>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_pipe_kernel<P, OCC>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, QkvPipe<P>::SMEM);
     return true;
   }();
   (void)attr;
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + P::BM - 1) / P::BM));
-  hipLaunchKernelGGL(qkv_pipe_kernel<P>, grid, dim3(256), QkvPipe<P>::SMEM, s, x, wqkv, qn_w, kn_w, rope_cos,
+  hipLaunchKernelGGL((qkv_pipe_kernel<P, OCC>), grid, dim3(256), QkvPipe<P>::SMEM, s, x, wqkv, qn_w, kn_w, rope_cos,
                      rope_sin, positions, int(T), int(S), int(H), int(Hq), int(Hkv), int(S_max), max_p, eps,
                      q_out, k_cache, v_cache);
   return hip_status("qmoe_qkv_norm_rope");
@@ -755,10 +755,17 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                        int(Hq), int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
     return hip_status("qmoe_qkv_norm_rope(finish)");
   }
-  if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32))
-    return qkv_pipe_launch<pipe::Pipe<256, 128, 64, 2>>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
-                                                         positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
-                                                         k_cache, v_cache, as_stream(stream));
+  if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32)) {
+    // 256-row tiles once they give every CU a workgroup; below that 128-row
+    // tiles, two per CU (a 640-token prompt: 200 workgroups instead of 120)
+    if ((T + 255) / 256 * (Hq + 2 * Hkv) >= 256)
+      return qkv_pipe_launch<pipe::Pipe<256, 128, 64, 2>, 1>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                              positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                              k_cache, v_cache, as_stream(stream));
+    return qkv_pipe_launch<pipe::Pipe<128, 128, 64, 2>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                            positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                            k_cache, v_cache, as_stream(stream));
+  }
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + tile::BM - 1) / tile::BM));
   hipLaunchKernelGGL(qkv_norm_rope_kernel, grid, dim3(256), 0, as_stream(stream), x, wqkv, q_norm_w,
                      k_norm_w, rope_cos, rope_sin, positions, int(T), int(S), int(H), int(Hq),

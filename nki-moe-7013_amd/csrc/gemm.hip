@@ -321,6 +321,117 @@ static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
   return launch_pipe<Tiny, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
 }
 
+// ------------------------------------------------------------------ split-K
+// For problems with too few output tiles to occupy the GPU (prefill-size
+// o_proj: 640 x 2048 with K = 4096 is 80 tiles of 128 x 128; the router
+// logits: 640 x 128 with K = 2048 is 20 tiles of 64 x 64), K is split into
+// `splits` slices: workgroup (tile, slice) writes its fp32 partial tile to a
+// caller-owned workspace part[slice][M][N], and splitk_reduce_kernel adds the
+// slices in slice order (fixed order: repeat calls are bit-identical) and
+// applies the epilogue mode.
+template <class P, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_splitk_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                               const uint16_t* __restrict__ B, int M, int N,
+                                                               int K, int splits, float* __restrict__ part) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int tiles_n = (N + P::BN - 1) / P::BN;
+  const int slice = int(blockIdx.x) % splits, tile = int(blockIdx.x) / splits;
+  const int m0 = (tile / tiles_n) * P::BM, n0 = (tile % tiles_n) * P::BN;
+  const int ks = K / splits;
+  const uint32_t k0b = uint32_t(slice) * uint32_t(ks) * 2u;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const pipe::i32x4 ra = pipe::make_rsrc(A, uint32_t((int64_t(M) - 1) * lda * 2 + int64_t(K) * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(B, uint32_t(int64_t(N) * K * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int rr = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(rr, lane);
+    if (j < P::AI)
+      vo[j] = m0 + rr < M ? uint32_t(int64_t(m0 + rr) * lda * 2) + k0b + c : pipe::PAD;
+    else
+      vo[j] = n0 + rr < N ? uint32_t(int64_t(n0 + rr) * K * 2) + k0b + c : pipe::PAD;
+  }
+  typename P::Acc acc;
+  P::run(ra, rb, vo, ks / P::BK, smem, acc);
+  float* dst = part + int64_t(slice) * M * N;
+#pragma unroll
+  for (int i = 0; i < P::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < P::FN; ++j) {
+      const int col = n0 + P::acc_col(wave, j, lane);
+      if (col < N) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + P::acc_row(wave, i, e, lane);
+          if (row < M) dst[int64_t(row) * N + col] = acc[i][j][e];
+        }
+      }
+    }
+}
+
+// C (mode) = sum over slices in order; 4 consecutive columns per thread.
+template <int MODE>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M,
+                                                           int N, void* C, int64_t ldc) {
+  const int64_t q = int64_t(blockIdx.x) * 256 + threadIdx.x;  // float4 index
+  const int64_t per_row = N / 4;
+  if (q >= int64_t(M) * per_row) return;
+  const int64_t row = q / per_row, col = (q - row * per_row) * 4;
+  const int64_t slab = int64_t(M) * N;
+  float4 v = *reinterpret_cast<const float4*>(part + row * N + col);
+  for (int s = 1; s < splits; ++s) {
+    const float4 w = *reinterpret_cast<const float4*>(part + s * slab + row * N + col);
+    v.x += w.x;
+    v.y += w.y;
+    v.z += w.z;
+    v.w += w.w;
+  }
+  store_out<MODE>(C, row * ldc + col, v.x);
+  store_out<MODE>(C, row * ldc + col + 1, v.y);
+  store_out<MODE>(C, row * ldc + col + 2, v.z);
+  store_out<MODE>(C, row * ldc + col + 3, v.w);
+}
+
+using SplitSmall = pipe::Pipe<128, 128, 64, 2>;
+using SplitTiny = pipe::Pipe<64, 64, 64, 4>;
+
+// Split-K plan for an M > 16 problem: 0 slices = do not split (the problem
+// already has at least 256 tiles, or K is too short to split).  small = 128 x
+// 128 tiles (at least 16 of them), else 64 x 64.  Slices double while the
+// grid stays within 512 workgroups and each slice keeps >= 512 (128 x 128)
+// or >= 256 (64 x 64) columns of K, a multiple of the 64-column stage.
+static int splitk_plan(int64_t M, int64_t N, int64_t K, bool* small) {
+  if (M <= 16 || N % 4 != 0 || K % 64 != 0) return 0;
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  *small = t128 >= 16;
+  const int64_t tiles = *small ? t128 : ((M + 63) / 64) * ((N + 63) / 64);
+  const int64_t kmin = *small ? 512 : 256;
+  if (tiles >= 256) return 0;
+  int splits = 1;
+  while (tiles * splits * 2 <= 512 && K % (int64_t(splits) * 2 * 64) == 0 && K / (splits * 2) >= kmin) splits *= 2;
+  return splits > 1 ? splits : 0;
+}
+
+template <class P, int MODE>
+static int launch_splitk(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K, int splits,
+                         float* part, void* C, int64_t ldc, hipStream_t s) {
+  static const bool attr = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_splitk_kernel<P, 2>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, P::SMEM);
+    return true;
+  }();
+  (void)attr;
+  const int64_t tiles = int64_t((M + P::BM - 1) / P::BM) * ((N + P::BN - 1) / P::BN);
+  hipLaunchKernelGGL((gemm_splitk_kernel<P, 2>), dim3(unsigned(tiles * splits)), dim3(256), P::SMEM, s, A, lda,
+                     B, M, N, K, splits, part);
+  if (int rc = hip_status("qmoe_gemm_ws(slices)")) return rc;
+  const int64_t n4 = int64_t(M) * (N / 4);
+  hipLaunchKernelGGL(splitk_reduce_kernel<MODE>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, s, part, splits,
+                     M, N, C, ldc);
+  return hip_status("qmoe_gemm_ws(reduce)");
+}
+
 // ------------------------------------------------------------------ launcher
 template <int MT, int MODE>
 static int launch_gemv_reg(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
@@ -512,4 +623,41 @@ extern "C" int qmoe_gemv_rmsnorm(const float* h, const qmoe_bf16* rms_w, float e
 extern "C" int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
                          int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream) {
   return qmoe::gemm_launch(A, lda, B, M, N, K, mode, C, ldc, qmoe::as_stream(stream));
+}
+
+extern "C" int64_t qmoe_gemm_ws_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0) return -1;
+  bool small = false;
+  const int splits = qmoe::splitk_plan(M, N, K, &small);
+  return splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
+}
+
+extern "C" int qmoe_gemm_ws(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+                            int64_t K, int mode, void* C, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                            qmoe_stream_t stream) {
+  using namespace qmoe;
+  bool small = false;
+  const int splits = splitk_plan(M, N, K, &small);
+  const int64_t need = splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
+  if (splits == 0 || workspace == nullptr || workspace_bytes < need || M >= (1ll << 31) || N >= (1ll << 31))
+    return gemm_launch(A, lda, B, M, N, K, mode, C, ldc, as_stream(stream));
+  QMOE_REQUIRE(A && B && C, "qmoe_gemm_ws: null pointer");
+  QMOE_REQUIRE(mode >= 0 && mode <= 2, "qmoe_gemm_ws: bad mode %d", mode);
+  QMOE_REQUIRE(lda >= K && ldc >= N && lda % 8 == 0, "qmoe_gemm_ws: bad lda/ldc");
+  QMOE_REQUIRE((M - 1) * lda * 2 + K * 2 < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "qmoe_gemm_ws: A or B larger than 2 GiB");
+  hipStream_t s = as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+#define QMOE_SPLIT(MODE)                                                                                 \
+  return small ? launch_splitk<SplitSmall, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C, ldc, s) \
+               : launch_splitk<SplitTiny, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C, ldc, s);
+  switch (mode) {
+    case QMOE_GEMM_STORE_BF16:
+      QMOE_SPLIT(QMOE_GEMM_STORE_BF16)
+    case QMOE_GEMM_STORE_F32:
+      QMOE_SPLIT(QMOE_GEMM_STORE_F32)
+    default:
+      QMOE_SPLIT(QMOE_GEMM_ADD_F32)
+  }
+#undef QMOE_SPLIT
 }

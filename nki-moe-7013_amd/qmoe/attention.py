@@ -133,5 +133,8 @@ class Attention:
                 self._ws[(B, cache.capacity)] = ws
             o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale, ws,
                                 max_ctx=max_ctx)
-        ops.gemm(o, self.wo, _lib.GEMM_ADD_F32, out=residual)
+        key = ("oproj", o.shape[0])
+        if key not in self._ws:  # split-K scratch for prefill-size token counts (None: not split)
+            self._ws[key] = ops.gemm_workspace(o.shape[0], self.wo.shape[0], self.wo.shape[1], x.device)
+        ops.gemm(o, self.wo, _lib.GEMM_ADD_F32, out=residual, workspace=self._ws[key])
         return residual

@@ -368,9 +368,20 @@ def moe_combine(
 
 
 # ----------------------------------------------------------------- GEMM
+def gemm_workspace(M: int, N: int, K: int, device) -> Optional[torch.Tensor]:
+    """Workspace for :func:`gemm` with split-K (``None`` when the shape is
+    not split: it already fills the GPU)."""
+    n = int(lib().qmoe_gemm_ws_workspace(M, N, K))
+    if n < 0:
+        raise ValueError("negative GEMM size")
+    return torch.empty(max(n // 4, 1), dtype=F32, device=device) if n > 0 else None
+
+
 def gemm(A: torch.Tensor, B: torch.Tensor, mode: int = _lib.GEMM_STORE_BF16,
-         out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``A[M,K] . B[N,K]^T`` with epilogue ``mode`` (store bf16 / store f32 / add f32)."""
+         out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``A[M,K] . B[N,K]^T`` with epilogue ``mode`` (store bf16 / store f32 / add f32).
+    With ``workspace`` (from :func:`gemm_workspace`) a problem with few output
+    tiles splits K over more workgroups (fixed-order, deterministic sum)."""
     if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
         raise ValueError("A must be [M,K] and B [N,K]")
     M, K = A.shape
@@ -383,6 +394,12 @@ def gemm(A: torch.Tensor, B: torch.Tensor, mode: int = _lib.GEMM_STORE_BF16,
         out = torch.empty(M, N, dtype=BF16 if mode == _lib.GEMM_STORE_BF16 else F32, device=A.device)
     _need(out, "out", BF16 if mode == _lib.GEMM_STORE_BF16 else F32, (M, N))
     _same_device(A, B, out)
+    if workspace is not None:
+        _need(workspace, "workspace", F32)
+        _same_device(A, workspace)
+        check(lib().qmoe_gemm_ws(_ptr(A), K, _ptr(B), M, N, K, int(mode), _ptr(out), N, _ptr(workspace),
+                                 workspace.numel() * 4, _stream()), "qmoe_gemm_ws")
+        return out
     check(lib().qmoe_gemm(_ptr(A), K, _ptr(B), M, N, K, int(mode), _ptr(out), N, _stream()), "qmoe_gemm")
     return out
 

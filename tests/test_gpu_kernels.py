@@ -54,6 +54,31 @@ def test_gemm_vs_fp32(dev, M, N, K):
     assert float(((cbf.float().cpu() - ref).abs() - ref.abs() * 2 ** -8).max()) <= 1e-4 * scale
 
 
+@pytest.mark.parametrize("M,N,K", [(640, 2048, 4096), (640, 128, 2048), (300, 200, 1024), (1000, 512, 2048)])
+def test_gemm_splitk_vs_fp32(dev, M, N, K):
+    """qmoe_gemm_ws: K split into slices through the workspace (the prefill
+    o_proj and router shapes), each mode vs fp32; repeats are bit-identical
+    (the slices are summed in a fixed order)."""
+    announce(f"gemm split-K M={M} N={N} K={K}")
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    A = bf16_randn((M, K), g, dev)
+    B = bf16_randn((N, K), g, dev, std=0.02)
+    ws = ops.gemm_workspace(M, N, K, dev)
+    assert ws is not None, "this shape should split K"
+    ref = A.float().cpu() @ B.float().cpu().t()
+    c32 = ops.gemm(A, B, _lib.GEMM_STORE_F32, workspace=ws)
+    c32b = ops.gemm(A, B, _lib.GEMM_STORE_F32, workspace=ws)
+    cbf = ops.gemm(A, B, _lib.GEMM_STORE_BF16, workspace=ws)
+    acc = torch.ones(M, N, device=dev)
+    ops.gemm(A, B, _lib.GEMM_ADD_F32, out=acc, workspace=ws)
+    torch.cuda.synchronize()
+    scale = float(ref.abs().max())
+    assert torch.equal(c32, c32b)
+    assert max_abs(c32, ref) <= 1e-4 * scale
+    assert max_abs(acc, ref + 1.0) <= 1e-4 * scale + 1e-6
+    assert float(((cbf.float().cpu() - ref).abs() - ref.abs() * 2 ** -8).max()) <= 1e-4 * scale
+
+
 # --------------------------------------------------------------------------- RMSNorm
 @pytest.mark.parametrize("rows", [1, 37, 640])
 def test_rmsnorm_residual(dev, rows):
