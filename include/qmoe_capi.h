@@ -53,6 +53,10 @@ typedef void* qmoe_stream_t;
 /* Largest row tile (tile_m of qmoe_moe_permute) qmoe_moe_experts_grouped takes. */
 #define QMOE_GROUPED_MAX_TILE_M 256
 
+/* Length of the dispatch `meta` array (i32): (n_tiles, n_active, error, -),
+ * then the work counters of qmoe_moe_experts_grouped. */
+#define QMOE_META_INTS 24
+
 /* Workgroups of the decode block's expert kernel (one per MI355X CU); sets
  * the size of its partial-output workspace. */
 #define QMOE_DECODE_BLOCK_WGS 256
@@ -93,9 +97,10 @@ int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float*
  *   expert-sorted slot, stable by token); token_slot: i32 [T*k] (slot of pair
  *   t*k+j); active: i32 [E] (experts with rows, ascending);
  *   tiles: i32 [max_tiles, 4] = (expert, slot_begin, slot_end, 0) in chunks of
- *   tile_m rows; meta: i32 [4] = (n_tiles, n_active, error, -): error is 1
- *   when an id is outside [0, E) (then n_tiles = n_active = 0 and the slot
- *   maps are the identity); meta[3] is not touched.
+ *   tile_m rows; meta: i32 [QMOE_META_INTS] = (n_tiles, n_active, error, -,
+ *   work counters): error is 1 when an id is outside [0, E) (then n_tiles =
+ *   n_active = 0 and the slot maps are the identity); meta[3] is not touched;
+ *   meta[4..23] are set to 0 (the grouped expert GEMMs' work queues).
  *   max_tiles = rows of `tiles`, at least ceil(T*k / tile_m) + E.  With
  *   max_tiles >= qmoe_moe_permute_tiles(T, k, E, tile_m) and T*k > 4096 the
  *   work is spread over one workgroup per 1024 pairs, using the rows past
@@ -204,8 +209,12 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   slot_token/tiles/meta from qmoe_moe_permute with tile_m <=
  *   QMOE_GROUPED_MAX_TILE_M (256 is the efficient choice: every tile is one
  *   256 x 256 MFMA tile, partial tiles run only their live 32-row blocks);
- *   max_tiles >= ceil(T*k / QMOE_GROUPED_MAX_TILE_M) + E (the grid size);
+ *   max_tiles >= ceil(T*k / QMOE_GROUPED_MAX_TILE_M) + E;
  *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
+ *   Work distribution: one persistent workgroup per CU takes (tile, weight
+ *   panel) items from per-XCD queues whose counters live in meta[4..21]
+ *   (zeroed by the permute; each kernel's last workgroup puts them back to
+ *   zero).  Calls that share one meta array must not overlap.
  *   Limits: H % 256 == 0, I % 128 == 0; x, act and one expert's w13 each
  *   below 2 GiB.
  * Replaces: _nki_cte_moe_left_gate_up_kernel qwen_with_nki.py:5341-5369 (left)
@@ -213,7 +222,7 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   _patched_torch_blockwise_matmul_inference 5872-6003. */
 int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_bf16* w2,
                              const int32_t* slot_token, const int32_t* tiles,
-                             const int32_t* meta, int64_t max_tiles, int64_t T, int64_t H,
+                             int32_t* meta, int64_t max_tiles, int64_t T, int64_t H,
                              int64_t I, int64_t E, int64_t k, qmoe_bf16* act,
                              qmoe_bf16* y_slot, qmoe_stream_t stream);
 

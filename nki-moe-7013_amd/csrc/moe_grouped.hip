@@ -1,10 +1,10 @@
 // Prefill-shape expert MLPs as two grouped GEMMs on bf16 MFMA.
 //
 // The row-tile table from qmoe_moe_permute (tile_m <= 256) lists, for every
-// expert, runs of at most 256 expert-sorted slots.  Each workgroup takes one
+// expert, runs of at most 256 expert-sorted slots.  Each item of work is one
 // (row tile, 256-row weight panel) pair on the direct-to-LDS pipeline of
 // mfma_wide.hpp (512 threads; A = 256 weight rows, B = up to 256 tokens; one
-// workgroup per CU).  Two pipelines share the grid, chosen per tile:
+// workgroup per CU).  Two pipelines share the kernel, chosen per tile:
 //   - more than 64 live rows: 256 x 256 x 32 stages, four deep, only the
 //     live 32-row token blocks computed;
 //   - at most 64 live rows (cold experts, where streaming the weights is the
@@ -23,11 +23,10 @@
 //   Both epilogues stage the bf16 tile through LDS (rows padded by 16 bytes)
 //   and write whole 16-byte chunks of contiguous output rows.
 //
-// Grid: one workgroup per (tile, panel) up to max_tiles; the live ones
-// (tile < meta[0]) are renumbered XCD-contiguously, panels fastest, so one
-// XCD works through consecutive tiles (mostly one expert at a time) and its
-// L2 serves that expert's weight panels and the tiles' token rows to all of
-// them.
+// Work distribution: persistent workgroups (one per CU) take (tile, panel)
+// items from per-XCD queues; see the queue helpers below.
+#include <atomic>
+
 #include "mfma_wide.hpp"
 
 namespace qmoe {
@@ -59,19 +58,69 @@ struct TileJob {
   int e, s0, rows, n0;
 };
 
-// Returns false for a workgroup beyond the live tiles.
-__device__ __forceinline__ bool tile_job(const int32_t* __restrict__ tiles,
-                                         const int32_t* __restrict__ meta, int npanels, TileJob& job) {
-  const int live = meta[0] * npanels;
-  const int hw = int(blockIdx.x);
-  if (hw >= live) return false;
-  const int item = pipe::xcd_contiguous(hw, live);
+// Work queues.  One persistent workgroup per CU takes (tile, weight panel)
+// items, tile-major with panels fastest.  XCD v owns the v-th of 8 equal
+// contiguous shares of the items and hands them out in order through its
+// counter, as the hardware dispatcher would: one XCD works through
+// consecutive tiles (mostly one expert at a time) and its L2 serves that
+// expert's weight panels and the tiles' token rows to all of them.  A
+// workgroup whose XCD has run dry takes the next item of another XCD's share,
+// so the XCDs finish together whatever the tiles cost (a hot expert's full
+// tiles take about twice as long as a cold expert's partial ones).
+// meta[META_CTR + 8 * kind + v] = items of share v handed out so far;
+// meta[META_DONE + kind] = workgroups finished.  The last workgroup to finish
+// puts both back to zero, so the next launch on the same meta starts clean.
+constexpr int META_CTR = 4, META_DONE = 20;
+static_assert(META_DONE + 2 <= QMOE_META_INTS, "work counters fit in meta");
+
+__device__ __forceinline__ int xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return int(v & 7);
+}
+
+// Next item for a workgroup on XCD x (its own share first), or -1 when every
+// share is handed out.  Thread 0 only.
+__device__ __forceinline__ int claim_item(int32_t* ctr, int live, int x) {
+  const int q = live >> 3, r = live & 7;
+  for (int i = 0; i < 8; ++i) {
+    const int v = (x + i) & 7;
+    const int n = q + (v < r ? 1 : 0);
+    if (n == 0) continue;
+    const int j = atomicAdd(ctr + v, 1);
+    if (j < n) return v * q + min(v, r) + j;
+  }
+  return -1;
+}
+
+// Item index for the whole workgroup (through LDS word 0, which no tile is
+// using between items), -1 when done.
+__device__ __forceinline__ int next_item(int32_t* ctr, int live, int x, uint8_t* smem) {
+  int* slot = reinterpret_cast<int*>(smem);
+  __syncthreads();  // the previous tile's epilogue has read its LDS
+  if (threadIdx.x == 0) slot[0] = claim_item(ctr, live, x);
+  __syncthreads();
+  const int item = slot[0];
+  __syncthreads();  // every wave has it before the next tile's DMA lands
+  return item;
+}
+
+__device__ __forceinline__ void finish_queue(int32_t* ctr, int32_t* done) {
+  if (threadIdx.x == 0 && atomicAdd(done, 1) == int(gridDim.x) - 1) {
+    // every other workgroup has made its last claim
+    for (int v = 0; v < 8; ++v) atomicExch(ctr + v, 0);
+    atomicExch(done, 0);
+  }
+}
+
+__device__ __forceinline__ TileJob job_of(int item, const int32_t* __restrict__ tiles, int npanels) {
+  TileJob job;
   const int t = item / npanels;
   job.n0 = (item - t * npanels) * PANEL;
   job.e = tiles[4 * t];
   job.s0 = tiles[4 * t + 1];
   job.rows = min(tiles[4 * t + 2] - job.s0, Hot::BN);
-  return true;
+  return job;
 }
 
 __device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) {
@@ -179,35 +228,57 @@ __device__ __forceinline__ void down_tile(const TileJob& job, const uint16_t* __
 
 __global__ __launch_bounds__(Hot::THREADS, 1) void moe_gateup_grouped_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w13,
-    const int32_t* __restrict__ slot_token, const int32_t* __restrict__ tiles,
-    const int32_t* __restrict__ meta, int T, int H, int I, uint16_t* __restrict__ act) {
+    const int32_t* __restrict__ slot_token, const int32_t* __restrict__ tiles, int32_t* meta, int T,
+    int H, int I, uint16_t* __restrict__ act) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  TileJob job;
-  if (!tile_job(tiles, meta, 2 * I / PANEL, job)) return;
-  if (job.rows <= COLD_MAX_ROWS)
-    gateup_tile<Cold>(job, x, w13, slot_token, T, H, I, act, smem);
-  else
-    gateup_tile<Hot>(job, x, w13, slot_token, T, H, I, act, smem);
+  const int npanels = 2 * I / PANEL, live = meta[0] * npanels, xcd = xcc_id();
+  int32_t* ctr = meta + META_CTR;
+  for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
+    const TileJob job = job_of(item, tiles, npanels);
+    if (job.rows <= COLD_MAX_ROWS)
+      gateup_tile<Cold>(job, x, w13, slot_token, T, H, I, act, smem);
+    else
+      gateup_tile<Hot>(job, x, w13, slot_token, T, H, I, act, smem);
+  }
+  finish_queue(ctr, meta + META_DONE);
 }
 
 __global__ __launch_bounds__(Hot::THREADS, 1) void moe_down_grouped_kernel(
     const uint16_t* __restrict__ act, const uint16_t* __restrict__ w2,
-    const int32_t* __restrict__ tiles, const int32_t* __restrict__ meta, int slots, int H, int I,
+    const int32_t* __restrict__ tiles, int32_t* meta, int slots, int H, int I,
     uint16_t* __restrict__ y_slot) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  TileJob job;
-  if (!tile_job(tiles, meta, H / PANEL, job)) return;
-  if (job.rows <= COLD_MAX_ROWS)
-    down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
-  else
-    down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
+  const int npanels = H / PANEL, live = meta[0] * npanels, xcd = xcc_id();
+  int32_t* ctr = meta + META_CTR + 8;
+  for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
+    const TileJob job = job_of(item, tiles, npanels);
+    if (job.rows <= COLD_MAX_ROWS)
+      down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
+    else
+      down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
+  }
+  finish_queue(ctr, meta + META_DONE + 1);
+}
+
+// Workgroups per grouped launch: one per CU (the kernels need all of a CU's
+// LDS), no more than there are items.
+unsigned grouped_grid(int64_t items) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return unsigned(std::max<int64_t>(1, std::min<int64_t>(n, items)));
 }
 
 }  // namespace qmoe
 
 extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13,
                                         const qmoe_bf16* w2, const int32_t* slot_token,
-                                        const int32_t* tiles, const int32_t* meta,
+                                        const int32_t* tiles, int32_t* meta,
                                         int64_t max_tiles, int64_t T, int64_t H, int64_t I,
                                         int64_t E, int64_t k, qmoe_bf16* act, qmoe_bf16* y_slot,
                                         qmoe_stream_t stream) {
@@ -233,7 +304,7 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
   }();
   (void)attr;
   hipStream_t s = as_stream(stream);
-  const unsigned g1 = unsigned(max_tiles * (2 * I / PANEL)), g2 = unsigned(max_tiles * (H / PANEL));
+  const unsigned g1 = grouped_grid(max_tiles * (2 * I / PANEL)), g2 = grouped_grid(max_tiles * (H / PANEL));
   hipLaunchKernelGGL(moe_gateup_grouped_kernel, dim3(g1), dim3(Hot::THREADS), SMEM, s, x, w13, slot_token,
                      tiles, meta, int(T), int(H), int(I), act);
   int rc = hip_status("qmoe_moe_experts_grouped(gate_up)");

@@ -12,7 +12,8 @@
 //                          for the expert totals, the earlier chunks for its
 //                          own bases) and runs the expert-level scans; chunk 0
 //                          writes counts, offsets, active list, tiles and
-//                          meta; each workgroup places its own chunk:
+//                          meta (work counters zeroed); each workgroup places
+//                          its own chunk:
 //                          slot = offsets[e] + (rows of e in earlier chunks)
 //                          + rank.
 // Both produce the same stable order: within an expert, increasing pair index.
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(PERM_THREADS) void permute_place_kernel(
   __shared__ int bad;
   const int t = threadIdx.x, c = blockIdx.x, nchunks = int(gridDim.x);
   const int c0 = c * PERM_CHUNK, n = min(PERM_CHUNK, N - c0);
+  if (c == 0) clear_work_counters(meta);
   if (t == 0) bad = 0;
   __syncthreads();
   for (int j = t; j < nchunks; j += PERM_THREADS)

@@ -43,8 +43,15 @@ __device__ __forceinline__ int block_scan_256(int v, int* carry) {
   return v + add;
 }
 
+// Zeroes the grouped expert GEMMs' work counters (meta[4..QMOE_META_INTS)).
+__device__ __forceinline__ void clear_work_counters(int32_t* meta) {
+  const int t = threadIdx.x;
+  if (t >= 4 && t < QMOE_META_INTS) meta[t] = 0;
+}
+
 // idx: expert id of pair s (N = T*k pairs).  Writes counts[E], offsets[E+1],
-// slot_token[N], token_slot[N], active[<=E], tiles[n_tiles][4], meta[0..2].
+// slot_token[N], token_slot[N], active[<=E], tiles[n_tiles][4], meta[0..2]
+// and zeroes meta[4..QMOE_META_INTS).
 template <int NT>
 __device__ void permute_block(const int32_t* idx, int N, int k, int E, int tile_m,
                               int32_t* counts, int32_t* offsets, int32_t* slot_token,
@@ -52,6 +59,7 @@ __device__ void permute_block(const int32_t* idx, int N, int k, int E, int tile_
                               int32_t* meta, PermuteSmem<NT>& sm) {
   constexpr int WAVES = NT / 64;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  clear_work_counters(meta);
   if (t < PERM_MAX_E) sm.count[t] = 0;
   if (t == 0) sm.bad = 0;
   __syncthreads();

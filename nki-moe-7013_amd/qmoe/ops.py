@@ -130,7 +130,7 @@ class Route:
     token_slot: torch.Tensor  # [T*k]
     active: torch.Tensor  # [E]
     tiles: torch.Tensor  # [rows >= max_tiles, 4]: the tile table, then permutation scratch
-    meta: torch.Tensor  # [4] = (n_tiles, n_active, error flag, unused)
+    meta: torch.Tensor  # [META_INTS] = (n_tiles, n_active, error flag, unused, grouped GEMM work counters)
     logits: Optional[torch.Tensor] = None  # [T, E] f32 (filled by moe_route)
     topk_idx: Optional[torch.Tensor] = None  # [T, k] i32
     topk_w: Optional[torch.Tensor] = None  # [T, k] f32
@@ -141,7 +141,7 @@ class Route:
         rows = int(lib().qmoe_moe_permute_tiles(T, k, E, tile_m))
         z = lambda *s: torch.empty(*s, dtype=I32, device=device)
         r = Route(T, k, E, tile_m, max_tiles, z(E), z(E + 1), z(T * k), z(T * k), z(E),
-                  z(max(rows, max_tiles), 4), z(4))
+                  z(max(rows, max_tiles), 4), z(_lib.META_INTS))
         if with_topk:
             r.logits = torch.empty(T, E, dtype=F32, device=device)
             r.topk_idx = z(T, k)

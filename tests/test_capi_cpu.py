@@ -34,6 +34,16 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib.PROTOTYPES), "ctypes prototypes out of sync with the header"
 
 
+def test_header_constants_match_python_mirror():
+    """Every numeric #define QMOE_X of the header that the Python side mirrors
+    as _lib.X has the same value (buffer sizes such as the meta length)."""
+    defs = dict(re.findall(r"^#define QMOE_(\w+) (\d+)", open(HEADER).read(), re.M))
+    mirrored = {k: v for k, v in defs.items() if hasattr(_lib, k)}
+    assert {"META_INTS", "GROUPED_MAX_TILE_M", "W2_BLOCK", "DECODE_BLOCK_WGS"} <= set(mirrored)
+    for k, v in mirrored.items():
+        assert getattr(_lib, k) == int(v), k
+
+
 def test_version():
     assert _lib.lib().qmoe_version() == 1
 

@@ -340,6 +340,35 @@ def test_experts_deterministic(dev, experts):
     assert torch.equal(outs[0], outs[1])
 
 
+def test_experts_grouped_route_reuse(dev, experts):
+    """The grouped GEMMs hand out work through counters in the route's meta;
+    the last workgroup of each launch puts them back to zero, so one route
+    serves any number of calls: every call into NaN-filled outputs writes all
+    of them, with the same bits as a call on a fresh route, and the counters
+    read zero afterwards."""
+    announce("grouped experts: one route, repeated calls")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(11)
+    T = 700
+    x1, x2 = bf16_randn((T, H), g, dev), bf16_randn((T, H), g, dev)
+    top = torch.from_numpy(_random_topk(T, K_TOP, E, 11, skew=1.1)).to(dev)
+    route = ops.moe_permute(top, E, 256)
+
+    def run(x, r):
+        act = torch.full((T * K_TOP, I), float("nan"), dtype=torch.bfloat16, device=dev)
+        y = torch.full((T * K_TOP, H), float("nan"), dtype=torch.bfloat16, device=dev)
+        return ops.moe_experts_grouped(x, w13, w2, r, act=act, y_slot=y)
+
+    ys = [run(x, route) for x in (x1, x2, x1, x2)]
+    fresh = [run(x, ops.moe_permute(top, E, 256)) for x in (x1, x2)]
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(ys[0]).all()) and bool(torch.isfinite(ys[1]).all())
+    assert torch.equal(ys[0], fresh[0]) and torch.equal(ys[2], fresh[0])
+    assert torch.equal(ys[1], fresh[1]) and torch.equal(ys[3], fresh[1])
+    assert not torch.equal(ys[0], ys[1])
+    assert int(route.meta[4:].abs().sum()) == 0
+
+
 @pytest.mark.parametrize("T", [1, 128])
 def test_moe_block_vs_oracle(dev, experts, router_w, T):
     """Full block: router -> permute -> experts -> combine vs oracle.moe_block."""
