@@ -215,7 +215,7 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   panel) items from per-XCD queues whose counters live in meta[4..21]
  *   (zeroed by the permute; each kernel's last workgroup puts them back to
  *   zero).  Calls that share one meta array must not overlap.
- *   Limits: H % 256 == 0, I % 128 == 0; x, act and one expert's w13 each
+ *   Limits: H % 256 == 0, I % 32 == 0; x, act and one expert's w13 each
  *   below 2 GiB.
  * Replaces: _nki_cte_moe_left_gate_up_kernel qwen_with_nki.py:5341-5369 (left)
  *   and _nki_cte_moe_down_scatter_kernel 4967-5040 (right), dispatched by

@@ -142,11 +142,16 @@ __device__ __forceinline__ void gateup_tile(const TileJob& job, const uint16_t* 
     const int r = P::dma_row(j, wave, lane);
     const uint32_t c = P::dma_chunk(r, lane);
     if (j < P::AI)
-      vo[j] = uint32_t(job.n0 + r) * uint32_t(H * 2) + c;
+      vo[j] = job.n0 + r < 2 * I ? uint32_t(job.n0 + r) * uint32_t(H * 2) + c : pipe::PAD;
     else
       vo[j] = r < job.rows ? uint32_t(slot_token[job.s0 + r]) * uint32_t(H * 2) + c : pipe::PAD;
   }
-  const int nbw = P::wave_blocks(wave, (job.rows + 31) / 32);
+  // The last panel holds 2I - n0 < 256 packed rows when 2I % 256 != 0: the
+  // waves whose 64 rows lie past 2I run no MFMAs (they still DMA and meet
+  // the barriers), and only the live units are stored.
+  const bool live_a = job.n0 + P::wave_arow(wave) < 2 * I;
+  const int nbw = live_a ? P::wave_blocks(wave, (job.rows + 31) / 32) : 0;
+  const int units = min(PANEL / 2, I - job.n0 / 2);
   typename P::Acc acc;
   P::run_dyn(nbw, ra, rb, vo, H / P::BK, smem, acc, uint32_t(P::BK * 2), uint32_t(P::BK * 2));
   // A block 0 = gate rows, block 1 = up rows of units n0/2 + 32 wm + [0, 32).  The
@@ -172,8 +177,9 @@ __device__ __forceinline__ void gateup_tile(const TileJob& job, const uint16_t* 
   }
   __syncthreads();
   uint16_t* dst = act + int64_t(job.s0) * I + job.n0 / 2;
-  for (int c = threadIdx.x; c < job.rows * (PANEL / 16); c += P::THREADS) {
-    const int r = c / (PANEL / 16), k = c % (PANEL / 16);
+  const int chunks = units / 8;
+  for (int c = threadIdx.x; c < job.rows * chunks; c += P::THREADS) {
+    const int r = c / chunks, k = c % chunks;
     *reinterpret_cast<uint4*>(dst + int64_t(r) * I + k * 8) = *reinterpret_cast<const uint4*>(tl + r * ACT_LD + k * 8);
   }
 }
@@ -231,7 +237,7 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_gateup_grouped_kernel(
     const int32_t* __restrict__ slot_token, const int32_t* __restrict__ tiles, int32_t* meta, int T,
     int H, int I, uint16_t* __restrict__ act) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const int npanels = 2 * I / PANEL, live = meta[0] * npanels, xcd = xcc_id();
+  const int npanels = (2 * I + PANEL - 1) / PANEL, live = meta[0] * npanels, xcd = xcc_id();
   int32_t* ctr = meta + META_CTR;
   for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
     const TileJob job = job_of(item, tiles, npanels);
@@ -252,7 +258,7 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_down_grouped_kernel(
   int32_t* ctr = meta + META_CTR + 8;
   for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
     const TileJob job = job_of(item, tiles, npanels);
-    if (job.rows <= COLD_MAX_ROWS)
+    if (job.rows <= COLD_MAX_ROWS && I % Cold::BK == 0)
       down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
     else
       down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
@@ -288,7 +294,7 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
   QMOE_REQUIRE(T >= 0 && T * k < (1ll << 30), "qmoe_moe_experts_grouped: bad T");
   QMOE_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= E, "qmoe_moe_experts_grouped: bad E/k");
   QMOE_REQUIRE(H % 256 == 0 && H > 0, "qmoe_moe_experts_grouped: H %% 256 != 0");
-  QMOE_REQUIRE(I % 128 == 0 && I > 0, "qmoe_moe_experts_grouped: I %% 128 != 0");
+  QMOE_REQUIRE(I % QMOE_W13_GROUP == 0 && I > 0, "qmoe_moe_experts_grouped: I %% 32 != 0");
   // every buffer the DMA reads must stay below 2 GiB (32-bit offsets, PAD above)
   QMOE_REQUIRE(T * H * 2 < (1ll << 31) && T * k * I * 2 < (1ll << 31) && 2 * I * H * 2 < (1ll << 31),
                "qmoe_moe_experts_grouped: operand larger than 2 GiB");
@@ -304,7 +310,7 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
   }();
   (void)attr;
   hipStream_t s = as_stream(stream);
-  const unsigned g1 = grouped_grid(max_tiles * (2 * I / PANEL)), g2 = grouped_grid(max_tiles * (H / PANEL));
+  const unsigned g1 = grouped_grid(max_tiles * ((2 * I + PANEL - 1) / PANEL)), g2 = grouped_grid(max_tiles * (H / PANEL));
   hipLaunchKernelGGL(moe_gateup_grouped_kernel, dim3(g1), dim3(Hot::THREADS), SMEM, s, x, w13, slot_token,
                      tiles, meta, int(T), int(H), int(I), act);
   int rc = hip_status("qmoe_moe_experts_grouped(gate_up)");

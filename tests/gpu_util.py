@@ -2,7 +2,11 @@
 
 import sys
 
+import numpy as np
 import torch
+
+import oracle
+from qmoe import weights
 
 # Parity bars (from the hot path's accuracy contract):
 #   layer / block outputs: max-abs <= 2e-2 and mean relative <= 5e-3 vs fp32
@@ -58,3 +62,39 @@ def routing_agreement(y_ref: torch.Tensor, router: torch.Tensor, k: int, ours_id
     gap = top.values[:, k - 1] - top.values[:, k]
     same = (top.indices[:, :k].sort(-1).values == ours_idx.long().sort(-1).values).all(-1)
     return same, gap
+
+
+def random_topk(T, k, E, seed, skew=None):
+    """Seeded top-k expert ids [T, k] (int32, distinct per row); with ``skew``,
+    expert popularity ~ rank^-skew over a random rank order."""
+    rng = np.random.default_rng(seed)
+    p = None
+    if skew is not None:
+        p = np.arange(1, E + 1, dtype=np.float64) ** (-skew)
+        p = p[rng.permutation(E)]
+        p /= p.sum()
+    return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+
+
+class ExpertCache:
+    """Unpacked (NxDI-layout) fp32 expert weights on the CPU, fetched lazily."""
+
+    def __init__(self, w13, w2):
+        self.w13, self.w2, self.c = w13, w2, {}
+
+    def __getitem__(self, e):
+        if e not in self.c:
+            gu = weights.unpack_gate_up(self.w13[e : e + 1]).float().cpu()[0]  # (H, 2I)
+            dn = weights.unpack_down(self.w2[e : e + 1]).float().cpu()[0]  # (I, H)
+            self.c[e] = (gu, dn)
+        return self.c[e]
+
+
+def oracle_rows(x, top_i, top_w, cache, rows):
+    """Oracle MoE output for selected token rows (decode schedule, 3456-3478)."""
+    out = []
+    for t in rows:
+        xs = x[t : t + 1].float()
+        acc = torch.stack([oracle.expert_swiglu(xs, *cache[int(e)])[0] for e in top_i[t]])
+        out.append(torch.sum(acc * top_w[t].float().unsqueeze(1), dim=0))
+    return torch.stack(out)

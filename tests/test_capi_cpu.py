@@ -59,7 +59,7 @@ def test_version():
         (lambda l: l.qmoe_router_topk(1, 1, None, 1, 2048, 128, 8, 1, 1, None, None), "null pointer"),
         (lambda l: l.qmoe_moe_permute(1, 4, 8, 128, 128, 10, 1, 1, 1, 1, 1, 1, 1, None), "max_tiles"),
         (lambda l: l.qmoe_moe_experts_gemv(1, 1, 1, 1, 1, 1, 1, 65, 2048, 768, 128, 8, 1, 1, None), "T must be"),
-        (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2048, 100, 128, 8, 1, 1, None), "I % 128"),
+        (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2048, 100, 128, 8, 1, 1, None), "I % 32"),
         (lambda l: l.qmoe_moe_experts_grouped(1, 1, 1, 1, 1, 1, 200, 4, 2176, 768, 128, 8, 1, 1, None), "H % 256"),
         (lambda l: l.qmoe_moe_combine(1, 0, 1, 1, None, 4, 8, 6, 1, None), "H % 4"),
         (lambda l: l.qmoe_embed(1, 100, 6, 1, 1, 1, 1, None), "H % 4 == 0"),

@@ -14,6 +14,9 @@ import torch
 
 import oracle
 from gpu_util import (GAP, announce, assert_close_layer, bf16_randn, gap_mask, max_abs, mean_rel)
+from gpu_util import ExpertCache as _ExpertCache
+from gpu_util import oracle_rows as _oracle_rows
+from gpu_util import random_topk as _random_topk
 
 from qmoe import _lib, ops, weights
 from qmoe.moe import MoEBlock
@@ -173,16 +176,6 @@ def test_router_topk_shapes(dev, T, E_, H_, k, with_bias):
 
 
 # --------------------------------------------------------------------------- permute
-def _random_topk(T, k, E, seed, skew=None):
-    rng = np.random.default_rng(seed)
-    p = None
-    if skew is not None:
-        p = np.arange(1, E + 1, dtype=np.float64) ** (-skew)
-        p = p[rng.permutation(E)]
-        p /= p.sum()
-    return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
-
-
 # T*k <= 4096 pairs: single-workgroup kernel; above: one workgroup per
 # 1024-pair chunk (513: 5 chunks, the last ragged; 16384: 128 chunks; 40000:
 # 313 chunks, ragged), or the single workgroup again when `tiles` holds only
@@ -232,30 +225,6 @@ def experts(dev):
     w13 = bf16_randn((E, 2 * I, H), g, dev, std=0.02)
     w2 = bf16_randn((E, I // 8, H, 8), g, dev, std=0.02)  # blocked layout (random values)
     return w13, w2
-
-
-class _ExpertCache:
-    """Unpacked (NxDI-layout) fp32 expert weights on the CPU, fetched lazily."""
-
-    def __init__(self, w13, w2):
-        self.w13, self.w2, self.c = w13, w2, {}
-
-    def __getitem__(self, e):
-        if e not in self.c:
-            gu = weights.unpack_gate_up(self.w13[e : e + 1]).float().cpu()[0]  # (H, 2I)
-            dn = weights.unpack_down(self.w2[e : e + 1]).float().cpu()[0]  # (I, H)
-            self.c[e] = (gu, dn)
-        return self.c[e]
-
-
-def _oracle_rows(x, top_i, top_w, cache, rows):
-    """Oracle MoE output for selected token rows (decode schedule, 3456-3478)."""
-    out = []
-    for t in rows:
-        xs = x[t : t + 1].float()
-        acc = torch.stack([oracle.expert_swiglu(xs, *cache[int(e)])[0] for e in top_i[t]])
-        out.append(torch.sum(acc * top_w[t].float().unsqueeze(1), dim=0))
-    return torch.stack(out)
 
 
 @pytest.mark.parametrize("T", [1, 8, 64, 128, 512, 4096])
