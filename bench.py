@@ -66,6 +66,8 @@ def parse():
                     help="only the T=4096 prefill MoE block (Zipf-skewed routing); prints its dict")
     ap.add_argument("--only-model", action="store_true",
                     help="time only the full model, in this process, and print its numbers as JSON")
+    ap.add_argument("--only-attention", action="store_true",
+                    help="only the B=8 attention layer (prefill 1024, decode at ctx 1280 and 8192); prints its dict")
     return ap.parse_args()
 
 
@@ -328,6 +330,16 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
 
     mean_ms, med_ms = event_time_experts(run_experts, 4 * L)
     flops = T * K_TOP * 2 * 3 * H * I
+    dense = None
+    if zipf_s:
+        # The same grouped GEMMs with every token on experts 0..7 (each expert
+        # T rows: only full 256 x 256 tiles, weights shared by T/256 tiles):
+        # the expert kernels' rate when MFMA work is all there is.
+        top = torch.arange(K_TOP, dtype=torch.int32, device=dev).repeat(T, 1)
+        droute = ops.moe_permute(top, E, TILE_M)
+        dmean, _ = event_time_experts(
+            lambda i: ops.moe_experts_grouped(xs[i % L], layers[i % L][1], layers[i % L][2], droute), 4 * L)
+        dense = {"experts_us_mean": dmean * 1e3, "experts_TFLOPs": flops / (dmean * 1e-3) / 1e12}
     us = ev_secs / done * 1e6
     # touched experts' weights once, the router, x in and the output, as bf16
     touched = float((torch.stack(counts) > 0).sum(1).float().mean())
@@ -345,6 +357,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         "experts_mfma_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "top_expert_share": float(cnt.max() / cnt.sum()),
         "routing_vs_zipf": hist,
+        "experts_dense_routing_8_experts": dense,
         "_cpu_case": (xs[0], biases[0]),  # layer 0's tokens and bias, for the CPU leg
     }
 
@@ -401,6 +414,33 @@ def measure_peaks(dev):
     e1.record()
     torch.cuda.synchronize()
     res["hbm_copy_GBps"] = round(2 * a.numel() * 2 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del a, b
+    # The vendor GEMM library (torch.matmul -> hipBLASLt) on dense bf16: the
+    # prefill experts' whole work at T = 4096 as one GEMM per projection (all
+    # T*k = 32768 (token, expert) rows against one weight: gate_up 32768 x 1536
+    # x 2048, down 32768 x 2048 x 768; no gather, no skew, no per-expert
+    # tiles), one expert's share at full load (4096 rows: too few tiles to
+    # fill 256 CUs), and 8192^3: what a tuned library reaches on this chip, as
+    # a ceiling beside the published peak.  Measurement only; the product
+    # never calls it.
+    lib_res = {}
+    for M, N, K in ((32768, 1536, 2048), (32768, 2048, 768), (4096, 1536, 2048), (4096, 2048, 768),
+                    (8192, 8192, 8192)):
+        A = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        B = torch.randn(K, N, generator=g, device=dev).to(torch.bfloat16)
+        C = torch.matmul(A, B)
+        reps = 20 if M * N * K < (1 << 34) else 5
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch.matmul(A, B, out=C)
+        e1.record()
+        torch.cuda.synchronize()
+        secs = e0.elapsed_time(e1) * 1e-3 / reps
+        lib_res[f"{M}x{N}x{K}"] = round(2.0 * M * N * K / secs / 1e12, 1)
+        del A, B, C
+    res["hipblaslt_bf16_TFLOPs"] = lib_res
     return res
 
 
@@ -776,7 +816,7 @@ def main():
         traffic_probe(a.tokens)
         return
     traffic = None
-    if not a.no_traffic and not a.only_model and not a.only_prefill and a.tokens <= 8:  # before this process touches the GPU
+    if not a.no_traffic and not (a.only_model or a.only_prefill or a.only_attention) and a.tokens <= 8:  # before this process touches the GPU
         traffic = measure_traffic(a.tokens)
         print(f"[bench] traffic: {traffic}", file=sys.stderr, flush=True)
     import torch
@@ -792,9 +832,16 @@ def main():
         print(json.dumps({"workload": "Qwen3-30B-A3B-shaped model, 48 layers, random-init bf16, batch 1, "
                                       "640-token prompt, 256 greedy steps", **res}))
         return
+    if a.only_attention:
+        res = bench_attention(dev)
+        res.pop("_weights")
+        print(f"[bench] attention: {res}", file=sys.stderr, flush=True)
+        print(json.dumps({"workload": "GQA attention layer, B=8, prefill 1024, decode at ctx 1280 and 8192", **res}))
+        return
     if a.only_prefill:
         layers = make_layers(min(a.layers, 4), dev)
         res = bench_prefill(layers, dev)
+        res.pop("_cpu_case")
         print(f"[bench] prefill: {res}", file=sys.stderr, flush=True)
         print(json.dumps({"workload": "Qwen3-30B-A3B MoE block, prefill T=4096, Zipf(1.1)-skewed routing, "
                                       "4 rotating layers", **res}))
@@ -832,6 +879,13 @@ def main():
     for key in ("prefill_T4096", "prefill_T128"):
         if key in extra:
             extra[key]["experts_frac_of_measured_mfma"] = extra[key]["experts_TFLOPs"] / peaks["mfma_bf16_random_TFLOPs"]
+    if "prefill_T4096" in extra:
+        # hipBLASLt's rate over the same work and flop mix (gate_up : down =
+        # 2 : 1) as one dense GEMM per projection: no gather, no skew
+        lr = peaks["hipblaslt_bf16_TFLOPs"]
+        lib_rate = 3.0 / (2.0 / lr["32768x1536x2048"] + 1.0 / lr["32768x2048x768"])
+        extra["prefill_T4096"]["experts_frac_of_hipblaslt_dense"] = round(
+            extra["prefill_T4096"]["experts_TFLOPs"] / lib_rate, 4)
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -868,6 +922,8 @@ def main():
                         "experts_mfma_frac": round(d["experts_mfma_frac"], 4),
                         "experts_frac_of_measured_mfma": round(d["experts_frac_of_measured_mfma"], 4),
                         "block_hbm_frac": round(d["block_hbm_frac"], 4), "cpu_tokens_per_s": cpu_of(name)}
+            if "experts_frac_of_hipblaslt_dense" in d:
+                tp[name]["experts_frac_of_hipblaslt_dense"] = d["experts_frac_of_hipblaslt_dense"]
     at = extra.get("attention_B8")
     if at:
         tp["attention_B8_prefill1024"] = {"tokens_per_s": round(at["prefill_tokens_per_s"], 1), "bound": "mfma",

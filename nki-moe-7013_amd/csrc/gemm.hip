@@ -5,10 +5,12 @@
 //    staged once in LDS; each wave streams R rows of B with 16-byte
 //    non-temporal loads (K/512 loads per row per lane, all in flight), and
 //    reduces the per-lane partial dots with cross-lane shuffles.
-//  * M > 16: the direct-to-LDS MFMA pipeline (mfma_pipe.hpp).
+//  * M > 16: the direct-to-LDS MFMA pipelines (mfma_pipe.hpp; from 224
+//    tiles of 256 x 256 on, the deep-staged 8-wave one of mfma_wide.hpp).
 #include "decode_util.hpp"
 #include "gemm.hpp"
 #include "mfma_pipe.hpp"
+#include "mfma_wide.hpp"
 
 namespace qmoe {
 
@@ -302,6 +304,95 @@ static int launch_pipe(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
   return hip_status("qmoe_gemm(tile)");
 }
 
+// ------------------------------------------------------------------ large GEMMs
+// Problems of at least 224 tiles of 256 x 256 run the grouped expert GEMMs'
+// mainloop (mfma_wide.hpp: 8 waves, four 32-column stages, three in flight).
+// Its A operand is B (weight rows n, 256 per tile) and its B operand is A
+// (rows m), so each lane holds one output row m and, per 32 x 32 block, runs
+// of 4 consecutive columns n: the epilogue stores them as one 16-byte fp32
+// (8-byte bf16) piece straight from the accumulators (N % 4 == 0, ldc % 4 ==
+// 0, C 16-byte aligned).  Tiles are walked as in gemm_pipe_kernel: XCD-
+// contiguous, in groups of 8 row tiles per column sweep.
+using WideDense = pipe::Wide<4, 2, 32, 4, 256>;
+
+template <int MODE>
+__device__ __forceinline__ void store_out4(void* C, int64_t idx, float a, float b, float c, float d) {
+  if constexpr (MODE == QMOE_GEMM_STORE_BF16) {
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(C) + idx) = make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
+  } else if constexpr (MODE == QMOE_GEMM_STORE_F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(C) + idx) = make_float4(a, b, c, d);
+  } else {
+    float4* p = reinterpret_cast<float4*>(reinterpret_cast<float*>(C) + idx);
+    const float4 v = *p;
+    *p = make_float4(v.x + a, v.y + b, v.z + c, v.w + d);
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(WideDense::THREADS, 1) void gemm_wide_kernel(const uint16_t* __restrict__ A,
+                                                                        int64_t lda,
+                                                                        const uint16_t* __restrict__ B, int M,
+                                                                        int N, int K, void* __restrict__ C,
+                                                                        int64_t ldc) {
+  using P = WideDense;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int gx = (N + P::BM - 1) / P::BM, gy = (M + P::BN - 1) / P::BN;
+  const int item = pipe::xcd_contiguous(int(blockIdx.x), gx * gy);
+  constexpr int GM = 8;
+  const int group = item / (GM * gx), first = group * GM, gm = min(gy - first, GM);
+  const int r = item - group * GM * gx;
+  const int m0 = (first + r % gm) * P::BN, n0 = (r / gm) * P::BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const pipe::i32x4 ra = pipe::make_rsrc(B, uint32_t(int64_t(N) * K * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(A, uint32_t((int64_t(M) - 1) * lda * 2 + int64_t(K) * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int rr = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(rr, lane);
+    if (j < P::AI)
+      vo[j] = n0 + rr < N ? uint32_t(int64_t(n0 + rr) * K * 2) + c : pipe::PAD;
+    else
+      vo[j] = m0 + rr < M ? uint32_t(int64_t(m0 + rr) * lda * 2) + c : pipe::PAD;
+  }
+  // this wave's live 32-row blocks of A rows (none when its weight rows lie past N)
+  const int nb = n0 + P::wave_arow(wave) < N ? P::wave_blocks(wave, (min(M - m0, P::BN) + 31) / 32) : 0;
+  typename P::Acc acc;
+  P::run_dyn(nb, ra, rb, vo, K / P::BK, smem, acc, uint32_t(P::BK * 2), uint32_t(P::BK * 2));
+#pragma unroll
+  for (int j = 0; j < P::FN; ++j) {
+    if (j >= nb) break;
+    const int row = m0 + P::acc_brow(wave, j, lane);
+    if (row >= M) continue;
+#pragma unroll
+    for (int i = 0; i < P::FM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + P::wave_arow(wave) + i * 32 + q * 8 + (lane >> 5) * 4;
+        if (col < N)
+          store_out4<MODE>(C, int64_t(row) * ldc + col, acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                           acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+      }
+  }
+}
+
+template <int MODE>
+static int launch_wide(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K, void* C,
+                       int64_t ldc, hipStream_t s) {
+  using P = WideDense;
+  static const bool attr = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_wide_kernel<MODE>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, P::SMEM);
+    return true;
+  }();
+  (void)attr;
+  const int64_t tiles = int64_t((M + P::BN - 1) / P::BN) * ((N + P::BM - 1) / P::BM);
+  hipLaunchKernelGGL((gemm_wide_kernel<MODE>), dim3(unsigned(tiles)), dim3(P::THREADS), P::SMEM, s, A, lda, B,
+                     M, N, K, C, ldc);
+  return hip_status("qmoe_gemm(wide)");
+}
+
 // Tile shape by how many tiles the problem has: 256x256 (one workgroup per
 // CU, least L2 traffic per flop) once it fills the GPU, else smaller tiles
 // with two workgroups per CU; problems that would still leave most CUs idle
@@ -315,6 +406,8 @@ static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
   using Small = pipe::Pipe<128, 128, 64, 2>;
   using Tiny = pipe::Pipe<64, 64, 64, 4>;
   auto count = [&](int bm, int bn) { return int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (count(256, 256) >= 224 && N % 4 == 0 && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0)
+    return launch_wide<MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (count(256, 256) >= 224) return launch_pipe<Big, 1, MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (count(128, 256) >= 224) return launch_pipe<Mid, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (count(128, 128) >= 96) return launch_pipe<Small, 2, MODE>(A, lda, B, M, N, K, C, ldc, s);

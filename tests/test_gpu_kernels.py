@@ -38,7 +38,11 @@ def _fp32_reference_matmuls():
                                    # ragged N; 128x256 tiles; 256x256 tiles
                                    (300, 200, 128), (4096, 2048, 1024), (4096, 4096, 256),
                                    # the prefill router shape (64x64 tiles, four stages)
-                                   (4096, 128, 2048)])
+                                   (4096, 128, 2048),
+                                   # from 224 tiles of 256x256: the 8-wave deep-staged pipeline
+                                   # (ragged M and N; the B=8 x 1024 o_proj shape), and the
+                                   # 256x256 two-stage one when N % 4 != 0
+                                   (7000, 2052, 512), (8192, 2048, 4096), (7000, 2050, 512)])
 def test_gemm_vs_fp32(dev, M, N, K):
     announce(f"gemm M={M} N={N} K={K}")
     g = torch.Generator(device=dev).manual_seed(M * 7 + N)
@@ -456,10 +460,10 @@ def _rope(max_pos, dev):
 
 
 # B*S <= 16: GEMV + finish path (8, 16: batched decode steps); up to 255 rows:
-# 128-row MFMA tiles; from 256 rows: the 256-row pipeline (3 x 257, 3 x 900:
-# ragged)
+# 128-row MFMA tiles; from 256 rows: the 256-row pipeline (3 x 257, 3 x 900,
+# 8 x 1000: ragged)
 @pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0), (8, 1, 1279), (16, 1, 40),
-                                       (1, 1, 0), (3, 900, 5), (2, 1024, 0), (1, 200, 3)])
+                                       (1, 1, 0), (3, 900, 5), (2, 1024, 0), (1, 200, 3), (8, 1000, 3)])
 def test_qkv_norm_rope(dev, attn_w, B, S, start):
     announce(f"qkv_norm_rope B={B} S={S} start={start}")
     wqkv, qn, kn = attn_w
@@ -483,6 +487,32 @@ def test_qkv_norm_rope(dev, attn_w, B, S, start):
     chk(kc[:, :, start : start + S], rk, "k cache")
     chk(vc[:, :, start : start + S], rv, "v cache")
     assert float(kc[:, :, :start].abs().sum()) == 0.0 and float(kc[:, :, start + S :].abs().sum()) == 0.0
+
+
+def test_qkv_norm_rope_wide_odd_heads(dev):
+    """Other head counts on the 256-row pipeline: 21 heads (7 q, 7 kv, odd)
+    and a ragged last token block (T = 5400), vs the oracle."""
+    Hq_, Hkv_, B, S, start = 7, 7, 1, 5400, 0
+    announce(f"qkv_norm_rope wide Hq={Hq_} Hkv={Hkv_} T={B * S}")
+    g = torch.Generator(device=dev).manual_seed(21)
+    wqkv = bf16_randn(((Hq_ + 2 * Hkv_) * D, H), g, dev, std=0.02)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    S_max = start + S + 3
+    x = bf16_randn((B * S, H), g, dev)
+    pos = (start + torch.arange(S, device=dev)).repeat(B).to(torch.int32)
+    cos, sin = _rope(S_max, dev)
+    kc = torch.zeros(B, Hkv_, S_max, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = ops.qkv_norm_rope(x, wqkv, qn, kn, cos, sin, pos, B, S, Hq_, Hkv_, kc, vc, 1e-6)
+    torch.cuda.synchronize()
+    wq, wk, wv = wqkv.float().cpu().split([Hq_ * D, Hkv_ * D, Hkv_ * D])
+    rq, rk, rv = oracle.qkv_norm_rope(x.cpu().view(B, S, H), wq, wk, wv, qn.cpu(), kn.cpu(),
+                                      pos.cpu().view(B, S).long(), Hq_, Hkv_, D, 1e-6, 1.0e6)
+    for a, r, what in ((q.view(B, S, Hq_, D).transpose(1, 2), rq, "q"), (kc[:, :, start : start + S], rk, "k"),
+                       (vc[:, :, start : start + S], rv, "v")):
+        err = (a.float().cpu() - r).abs() - r.abs() * 2 ** -8  # one bf16 rounding
+        assert float(err.max()) <= 2e-4, what
 
 
 @pytest.mark.parametrize("B,S,start", [(2, 200, 0), (1, 1024, 0), (2, 70, 130), (8, 64, 0)])
