@@ -441,6 +441,99 @@ def measure_peaks(dev):
         lib_res[f"{M}x{N}x{K}"] = round(2.0 * M * N * K / secs / 1e12, 1)
         del A, B, C
     res["hipblaslt_bf16_TFLOPs"] = lib_res
+    res.update(measure_hw_probes(dev, lib))
+    return res
+
+
+def measure_hw_probes(dev, lib):
+    """The probe library's hardware ceilings (probes/hw.hip): the cost of a
+    kernel boundary inside a HIP graph, the HBM read rate at 256 and 1024
+    workgroups on a 76 MB working set (the decode block's), rotated over 1 GiB
+    so the 256 MB Infinity Cache cannot serve it, and the L2 -> CU read rate
+    into VGPRs and through the LDS DMA."""
+    import ctypes
+
+    import torch
+
+    P, I64, INT = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.qmoe_probe_empty.argtypes, lib.qmoe_probe_empty.restype = [INT, P], INT
+    lib.qmoe_probe_stream.argtypes, lib.qmoe_probe_stream.restype = [P, I64, INT, P, P], INT
+    lib.qmoe_probe_l2.argtypes, lib.qmoe_probe_l2.restype = [P, INT, INT, INT, P, P], INT
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(f"probe launch failed ({rc})")
+
+    def graph_us(fn, n, reps=5):
+        """Per-launch microseconds of n launches of fn() captured in one graph."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(n):
+                fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n)
+
+    out = torch.empty(4096, dtype=torch.int32, device=dev)
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    small = torch.ones(1 << 22, dtype=torch.uint8, device=dev)  # 4 MB
+    res["graph_launch_us"] = {
+        "empty_1wg": round(graph_us(lambda: ok(lib.qmoe_probe_empty(1, cur())), 200), 3),
+        "read_4MB_1024wg": round(graph_us(lambda: ok(lib.qmoe_probe_stream(
+            ctypes.c_void_p(small.data_ptr()), small.numel(), 1024, ctypes.c_void_p(out.data_ptr()), cur())), 200), 3),
+    }
+    del small
+    window = 18560 * 4096  # 76,021,760 bytes: the decode block's touched weights at T = 1
+    big = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    n_win = big.numel() // window
+    res["hbm_read_76MB_GBps"] = {}
+    for blocks in (256, 1024):
+        def rotate():
+            for w in range(n_win):
+                ok(lib.qmoe_probe_stream(ctypes.c_void_p(big.data_ptr() + w * window), window, blocks,
+                                         ctypes.c_void_p(out.data_ptr()), cur()))
+        rotate()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            rotate()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (3 * n_win)
+        res["hbm_read_76MB_GBps"][f"{blocks}wg"] = round(window / (us * 1e-6) / 1e9, 1)
+        res["hbm_read_76MB_GBps"][f"{blocks}wg_us"] = round(us, 2)
+    del big
+    l2 = torch.ones(512 * 1024, dtype=torch.uint8, device=dev)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    res["l2_read_TBps"] = {}
+    for name, dma in (("vgpr", 0), ("lds_dma", 1)):
+        blocks, iters = n_cu, 2048
+        launch = lambda: ok(lib.qmoe_probe_l2(ctypes.c_void_p(l2.data_ptr()), blocks, iters, dma,
+                                              ctypes.c_void_p(out.data_ptr()), cur()))
+        launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        secs = e0.elapsed_time(e1) * 1e-3 / 5
+        res["l2_read_TBps"][name] = round(blocks * 4 * iters * 8192 / secs / 1e12, 2)
     return res
 
 
