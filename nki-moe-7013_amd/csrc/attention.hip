@@ -277,17 +277,36 @@ __device__ __forceinline__ int vt_slot(int key) {
 // start_dev, when not null, holds the chunk start in device memory (read here,
 // clamped into [0, S_max - S]) so a captured graph can replay the same
 // launch at a new position; otherwise `start` is used.
+//
+// Software pipeline over the 64-key steps: the S^T MFMAs of step kt+1 are
+// issued before the softmax and the O^T MFMAs of step kt, so the softmax's
+// VALU work runs while the matrix pipe is busy.  K is double-buffered in LDS
+// (the next step's tile is read while this step's V is), V single-buffered;
+// two barriers per step:
+//   A (loop top)  K(kt+1) and V(kt) are in LDS; every wave is done with the
+//                 K buffer that held K(kt);
+//   B             every wave is done reading V(kt).
+// K(kt+2) is stored into the free K buffer before B and V(kt+1) after it,
+// each from registers loaded one step earlier.  K and V rows come through
+// buffer loads whose range ends at kv_end, so rows past it read as zeros.
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int S, int Hq, int Hkv, int S_max, int start,
     const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out) {
   if (start_dev) start = min(max(start_dev[0], 0), S_max - S);
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[AP_KT * AP_LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AP_KT * AP_LDK];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * AP_LDV];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int qt = gridDim.x - 1 - blockIdx.x;  // heavy (late) query tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int kvh = h / (Hq / Hkv);
+  // One-dimensional grid in bands of one query tile each, the heaviest (latest)
+  // tile first, so the long workgroups start first and the short ones fill
+  // the end.  Inside a band, item r = hin * (B * Hkv) + (b * Hkv + kvh): the q
+  // heads sharing a kv head sit B * Hkv items apart, i.e. on one XCD when
+  // B * Hkv is a multiple of 8 (workgroup i runs on XCD i % 8), whose L2
+  // then serves their K/V tiles.
+  const int n_qt = (S + AP_QT - 1) / AP_QT, G = Hq / Hkv, n_grp = int(gridDim.x) / n_qt / G;
+  const int qt = n_qt - 1 - int(blockIdx.x) / (n_grp * G);
+  const int r_band = int(blockIdx.x) % (n_grp * G), grp = r_band % n_grp;
+  const int kvh = grp % Hkv, b = grp / Hkv, h = kvh * G + r_band / n_grp;
   const int q0 = qt * AP_QT;
   const int qrow = q0 + wave * 32 + (lane & 31);  // this lane's query (column of S^T)
   const int hl = lane >> 5;
@@ -324,38 +343,44 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   const int wave_first = start + q0 + wave * 32;
   const int wave_last = min(wave_first + 31, kv_end - 1);
 
-  // One K/V tile per step, prefetched into registers during the previous
-  // step's MFMAs.  K: chunk c = t + 256 j (key c / 16, dims (c % 16) * 8).
-  // V: item i = t + 256 j: key pair kp = i % 32 (keys 2kp, 2kp + 1, which sit
-  // in adjacent slots of the permuted V^T row) and dim chunk i / 32, so the
+  // Tile loads.  K: chunk c = t + 256 j (key c / 16, dims (c % 16) * 8).  V:
+  // item i = t + 256 j: key pair kp = i % 32 (keys 2kp, 2kp + 1, which sit in
+  // adjacent slots of the permuted V^T row) and dim chunk i / 32, so the
   // transpose into LDS is 32-bit (key pair) writes, the 32 key pairs of a
   // wave half on distinct banks.
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(k_cache + kv_base), short(0), kv_end * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(v_cache + kv_base), short(0), kv_end * HD * 2, 0x00020000);
   u32x4 kreg[4], vreg[2][2];
-  auto gload = [&](int kt) {
-    const int kv0 = kt * AP_KT;
+  auto gload_k = [&](int kt) {
+    const int so = kt * AP_KT * HD * 2;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = t + 256 * j, key = c >> 4, dc = (c & 15) * 8;
-      kreg[j] = kv0 + key < kv_end ? ld16(k_cache + kv_base + int64_t(kv0 + key) * HD + dc)
-                                   : u32x4{0u, 0u, 0u, 0u};
+      const int c = t + 256 * j;
+      kreg[j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c >> 4) * HD + (c & 15) * 8) * 2, so, 0));
     }
+  };
+  auto gload_v = [&](int kt) {
+    const int so = kt * AP_KT * HD * 2;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int key = 2 * kp + r;
-        vreg[j][r] = kv0 + key < kv_end ? ld16(v_cache + kv_base + int64_t(kv0 + key) * HD + dc)
-                                        : u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int r = 0; r < 2; ++r)
+        vreg[j][r] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ((2 * kp + r) * HD + dc) * 2, so, 0));
     }
   };
-  auto lstore = [&]() {
+  auto lstore_k = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = t + 256 * j, key = c >> 4, dc = (c & 15) * 8;
-      *reinterpret_cast<u32x4*>(Ks + key * AP_LDK + dc) = kreg[j];
+      *reinterpret_cast<u32x4*>(Ks[buf] + key * AP_LDK + dc) = kreg[j];
     }
+  };
+  auto lstore_v = [&]() {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
@@ -369,30 +394,34 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
       }
     }
   };
-  if (n_kt > 0) gload(0);
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int kv0 = kt * AP_KT;
-    __syncthreads();  // the previous step's LDS reads are done
-    lstore();
-    if (kt + 1 < n_kt) gload(kt + 1);
-    __syncthreads();
-    if (kv0 > wave_last) continue;  // past this wave's queries (wave-uniform)
-    // S^T blocks: keys [0,32) and [32,64) x this wave's 32 queries; a block
-    // wholly past the wave's last query is skipped (its scores are -inf)
-    const bool live1 = kv0 + 32 <= wave_last;
-    f32x16 st[2];
+  // S^T blocks of the tile at kv0 (in K buffer buf): keys [0,32) and [32,64)
+  // x this wave's 32 queries, the two MFMA chains interleaved; a block wholly
+  // past the wave's last query is not computed (left 0, masked below)
+  auto qk = [&](int buf, int kv0, f32x16 (&st)[2]) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
-      if (kb == 1 && !live1) break;
-      const uint16_t* kp = Ks + (kb * 32 + (lane & 31)) * AP_LDK + hl * 8;
+    const uint16_t* kp = Ks[buf] + (lane & 31) * AP_LDK + hl * 8;
+    if (kv0 + 32 <= wave_last) {
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(kp + ks * 16);
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], st[kb], 0, 0, 0);
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ks * 16);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kp + 32 * AP_LDK + ks * 16);
+        st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
+        st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], st[1], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ks * 16);
+        st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
       }
     }
+  };
+  // softmax of the tile at kv0 and O^T += V^T P^T (V^T of this tile in LDS)
+  auto softmax_pv = [&](int kv0, f32x16 (&st)[2]) {
+    const bool live1 = kv0 + 32 <= wave_last;
     // causal / range mask only where a tile reaches past the wave's first query
     if (kv0 + AP_KT - 1 > wave_first || kv0 + AP_KT > kv_end) {
 #pragma unroll
@@ -411,7 +440,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     for (int i = 2; i < 16; ++i) mloc = fmaxf(mloc, st[0][i]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, st[1][i]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
+    {  // max with lane l ^ 32 (the other half of the same query's keys)
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
+      mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
+    }
     const bool grow = mloc > m_run + AP_TAU;
     if (__builtin_amdgcn_ballot_w64(grow)) {
       const float m_new = grow ? mloc : m_run;
@@ -449,8 +481,47 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[db], 0, 0, 0);
       }
     }
+  };
+
+  f32x16 sc[2], sn[2];
+  if (n_kt > 0) {
+    gload_k(0);
+    gload_v(0);
+    lstore_k(0);
+    lstore_v();
+    if (n_kt > 1) {
+      gload_k(1);
+      gload_v(1);
+    }
+    __syncthreads();  // K(0), V(0) visible
+    if (0 <= wave_last) qk(0, 0, sc);
+    if (n_kt > 1) lstore_k(1);
+    if (n_kt > 2) gload_k(2);
   }
-  l_run += __shfl_xor(l_run, 32, 64);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int kv0 = kt * AP_KT;
+    __syncthreads();  // A: K(kt+1), V(kt) visible; K(kt)'s buffer is free
+    const bool next_live = kt + 1 < n_kt && kv0 + AP_KT <= wave_last;
+    if (next_live) qk((kt + 1) & 1, kv0 + AP_KT, sn);
+    if (kv0 <= wave_last) softmax_pv(kv0, sc);  // past this wave's queries: nothing (wave-uniform)
+    if (kt + 2 < n_kt) {
+      lstore_k(kt & 1);
+      if (kt + 3 < n_kt) gload_k(kt + 3);
+    }
+    __syncthreads();  // B: every wave is done reading V(kt)
+    if (kt + 1 < n_kt) {
+      lstore_v();
+      if (kt + 2 < n_kt) gload_v(kt + 2);
+    }
+    if (next_live) {
+      sc[0] = sn[0];
+      sc[1] = sn[1];
+    }
+  }
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   if (qrow >= S) return;
   const float inv = 1.0f / l_run;
   uint16_t* op = out + ((int64_t(b) * S + qrow) * Hq + h) * HD;
@@ -803,7 +874,8 @@ extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && start >= 0 && start + S <= S_max,
                "qmoe_attn_prefill: need 0 <= start and start + S <= S_max");
   if (B == 0 || S == 0) return QMOE_OK;
-  dim3 grid(unsigned((S + AP_QT - 1) / AP_QT), unsigned(Hq), unsigned(B));
+  QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill: grid too large");
+  const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
                      int(S), int(Hq), int(Hkv), int(S_max), int(start), nullptr, scale_log2, out);
@@ -818,7 +890,8 @@ extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill_at: bad heads");
   QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max, "qmoe_attn_prefill_at: need S <= S_max");
   if (B == 0 || S == 0) return QMOE_OK;
-  dim3 grid(unsigned((S + AP_QT - 1) / AP_QT), unsigned(Hq), unsigned(B));
+  QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill_at: grid too large");
+  const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
                      int(S), int(Hq), int(Hkv), int(S_max), 0, start, scale_log2, out);
