@@ -323,7 +323,7 @@ int64_t qmoe_qkv_norm_rope_workspace(int64_t T, int64_t H, int64_t Hq, int64_t H
 /* Causal GQA flash attention for a prefill chunk.  Query s of batch b sits at
  * cache index start + s and sees cache entries [0, start + s].
  *   q: bf16 [B*S, Hq, D]; k_cache, v_cache: bf16 [B, Hkv, S_max, D];
- *   out: bf16 [B*S, Hq*D].  Limits: D == 128, Hq % Hkv == 0.
+ *   out: bf16 [B*S, Hq*D].  Limits: D == 128, Hq % Hkv == 0, S_max <= 2^22.
  * Replaces: the NxDI attention base's context-encoding attention
  *   (flash kernel attention_isa_kernel, qwen_with_nki.py:25-28, 1251). */
 int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,

@@ -9,9 +9,10 @@
 //                    transposed, S^T = K . Q^T, so each lane owns one query
 //                    column: row max / row sum are lane-local plus one
 //                    exchange with lane^32, and the probabilities already sit
-//                    in the B-operand layout of O^T = V^T . P^T (the key order
-//                    inside each 16-key MFMA step is permuted to match; V is
-//                    stored transposed in LDS in that order).
+//                    in the B-operand layout of O^T = V^T . P^T.  K and V
+//                    tiles reach LDS by DMA, row-major; the V^T fragments
+//                    come from transposing LDS reads (ds_read_b64_tr_b16) in
+//                    the key order of the P^T registers.
 //  attn_decode    -- split-KV flash decoding on MFMA: a wave owns 64 keys of
 //                    one (batch, kv head) and all q heads of that GQA group
 //                    (S^T = K.Q^T, softmax per column, O^T = V^T.P^T), so each
@@ -261,42 +262,58 @@ static int qkv_pipe_launch(const uint16_t* x, const uint16_t* wqkv, const uint16
 }
 
 // ====================================================================== prefill
-constexpr int AP_QT = 128;      // query rows per workgroup (4 waves x 32)
-constexpr int AP_KT = 64;       // keys per step
-constexpr int AP_LDK = HD + 8;  // K tile row stride (bf16)
-constexpr int AP_LDV = AP_KT + 8;
-constexpr float AP_TAU = 8.0f;  // lazy-max slack (log2 units): p < 2^8 between rescales
+constexpr int AP_QT = 128;               // query rows per workgroup (4 waves x 32)
+constexpr int AP_KT = 64;                // keys per step
+constexpr int AP_ROWB = HD * 2;          // bytes per K / V row in LDS (no pad: chunks are swizzled)
+constexpr int AP_TILE = AP_KT * AP_ROWB;  // 16 KB per K or V tile
+constexpr float AP_TAU = 8.0f;           // lazy-max slack (log2 units): p < 2^8 between rescales
+// The tile DMAs address a (batch, kv head) cache slice with 32-bit byte
+// offsets: (S_max + AP_KT) * AP_ROWB must stay below 2^31.
+constexpr int AP_MAX_SMAX = 1 << 22;
 
-// position of key r (0..63) inside the permuted, transposed V tile row
-__device__ __forceinline__ int vt_slot(int key) {
-  const int s = key >> 4, r = key & 15;
-  const int h = (r >> 2) & 1, jj = (r >> 3) * 4 + (r & 3);
-  return s * 16 + h * 8 + jj;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// LDS slot of the 16-byte chunk c of K row r.  A fragment read (ds_read_b128)
+// takes one chunk of 16 consecutive rows; r % 16 puts them on 16 distinct
+// bank groups.
+__device__ __forceinline__ int ap_kslot(int r, int c) { return c ^ (r & 15); }
+// LDS slot of chunk c of V row r.  A transposing read (ds_read_b64_tr_b16)
+// covers, per half-wave, 4 consecutive rows (4-aligned) x 4 consecutive
+// chunks (4-aligned), and per 16-lane group 4 rows x 2 chunks; this XOR keeps
+// both on distinct bank groups.
+__device__ __forceinline__ int ap_vslot(int r, int c) { return c ^ (4 * (r & 3) + 2 * ((r >> 1) & 1)); }
+
+// ds_read_b64_tr_b16: each group of 16 lanes reads a block of 16 x 4 bf16
+// (lane j supplies the address of row j: 4 consecutive elements) and lane i
+// receives column i % 4 of rows i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12.
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
 }
 
 // start_dev, when not null, holds the chunk start in device memory (read here,
 // clamped into [0, S_max - S]) so a captured graph can replay the same
 // launch at a new position; otherwise `start` is used.
 //
-// Software pipeline over the 64-key steps: the S^T MFMAs of step kt+1 are
-// issued before the softmax and the O^T MFMAs of step kt, so the softmax's
-// VALU work runs while the matrix pipe is busy.  K is double-buffered in LDS
-// (the next step's tile is read while this step's V is), V single-buffered;
-// two barriers per step:
-//   A (loop top)  K(kt+1) and V(kt) are in LDS; every wave is done with the
-//                 K buffer that held K(kt);
-//   B             every wave is done reading V(kt).
-// K(kt+2) is stored into the free K buffer before B and V(kt+1) after it,
-// each from registers loaded one step earlier.  K and V rows come through
-// buffer loads whose range ends at kv_end, so rows past it read as zeros.
+// K and V tiles go global -> LDS by DMA (`buffer_load_dwordx4 ... lds`, no
+// VGPR staging), both row-major with swizzled chunks, double-buffered.  S^T =
+// K . Q^T reads K fragments with ds_read_b128; O^T = V^T . P^T reads its V^T
+// fragments straight out of the row-major V tile with the transposing LDS
+// read, in the key order of the P^T registers (no transposed copy of V).
+// Per 64-key step kt: the S^T MFMAs of step kt+1 are issued before the
+// softmax and the O^T MFMAs of step kt, so the softmax's VALU work runs while
+// the matrix pipe is busy; then one barrier, after which K(kt+3) and V(kt+2)
+// are DMA'd into the buffers that K(kt+1) and V(kt) just left.  The DMA
+// sources are range-checked buffer loads ending at kv_end, so rows past the
+// visible range read as zeros.
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, int S, int Hq, int Hkv, int S_max, int start,
     const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out) {
   if (start_dev) start = min(max(start_dev[0], 0), S_max - S);
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][AP_KT * AP_LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * AP_LDV];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * AP_TILE];  // K0, K1, V0, V1
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   // One-dimensional grid in bands of one query tile each, the heaviest (latest)
   // tile first, so the long workgroups start first and the short ones fill
   // the end.  Inside a band, item r = hin * (B * Hkv) + (b * Hkv + kvh): the q
@@ -343,84 +360,77 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   const int wave_first = start + q0 + wave * 32;
   const int wave_last = min(wave_first + 31, kv_end - 1);
 
-  // Tile loads.  K: chunk c = t + 256 j (key c / 16, dims (c % 16) * 8).  V:
-  // item i = t + 256 j: key pair kp = i % 32 (keys 2kp, 2kp + 1, which sit in
-  // adjacent slots of the permuted V^T row) and dim chunk i / 32, so the
-  // transpose into LDS is 32-bit (key pair) writes, the 32 key pairs of a
-  // wave half on distinct banks.
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(k_cache + kv_base), short(0), kv_end * HD * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(v_cache + kv_base), short(0), kv_end * HD * 2, 0x00020000);
-  u32x4 kreg[4], vreg[2][2];
-  auto gload_k = [&](int kt) {
-    const int so = kt * AP_KT * HD * 2;
+  // DMA: wave w writes rows [16w, 16w + 16) of each K / V tile with four
+  // instructions of 4 rows (1 KB of LDS each); lane j fills slot j % 16 of row
+  // 16w + 4i + j / 16, so it fetches the chunk whose swizzled slot that is
+  // (both swizzles are XOR involutions).
+  const pipe::i32x4 rk = pipe::make_rsrc(k_cache + kv_base, uint32_t(kv_end) * AP_ROWB);
+  const pipe::i32x4 rv = pipe::make_rsrc(v_cache + kv_base, uint32_t(kv_end) * AP_ROWB);
+  uint32_t koff[4], voff[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = t + 256 * j;
-      kreg[j] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, ((c >> 4) * HD + (c & 15) * 8) * 2, so, 0));
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wave + 4 * i + (lane >> 4), s = lane & 15;
+    koff[i] = uint32_t(r * AP_ROWB + ap_kslot(r, s) * 16);
+    voff[i] = uint32_t(r * AP_ROWB + ap_vslot(r, s) * 16);
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(smem));
+  auto dma_k = [&](int kt, int buf) {
+    const uint32_t dst = lds0 + uint32_t(buf * AP_TILE + wave * 4096), adv = uint32_t(kt) * AP_TILE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pipe::dma16(dst + i * 1024, koff[i] + adv, rk, 0);
   };
-  auto gload_v = [&](int kt) {
-    const int so = kt * AP_KT * HD * 2;
+  auto dma_v = [&](int kt, int buf) {
+    const uint32_t dst = lds0 + uint32_t((2 + buf) * AP_TILE + wave * 4096), adv = uint32_t(kt) * AP_TILE;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-        vreg[j][r] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, ((2 * kp + r) * HD + dc) * 2, so, 0));
-    }
+    for (int i = 0; i < 4; ++i) pipe::dma16(dst + i * 1024, voff[i] + adv, rv, 0);
   };
-  auto lstore_k = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = t + 256 * j, key = c >> 4, dc = (c & 15) * 8;
-      *reinterpret_cast<u32x4*>(Ks[buf] + key * AP_LDK + dc) = kreg[j];
-    }
-  };
-  auto lstore_v = [&]() {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = t + 256 * j, kp = i & 31, dc = (i >> 5) * 8;
-      const int vs = vt_slot(2 * kp);  // even; key 2kp + 1 is at vs + 1
-      const uint32_t a4[4] = {vreg[j][0].x, vreg[j][0].y, vreg[j][0].z, vreg[j][0].w};
-      const uint32_t b4[4] = {vreg[j][1].x, vreg[j][1].y, vreg[j][1].z, vreg[j][1].w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        *reinterpret_cast<uint32_t*>(Vt + (dc + 2 * u) * AP_LDV + vs) = (a4[u] & 0xffffu) | (b4[u] << 16);
-        *reinterpret_cast<uint32_t*>(Vt + (dc + 2 * u + 1) * AP_LDV + vs) = (a4[u] >> 16) | (b4[u] & 0xffff0000u);
-      }
-    }
-  };
+
   // S^T blocks of the tile at kv0 (in K buffer buf): keys [0,32) and [32,64)
   // x this wave's 32 queries, the two MFMA chains interleaved; a block wholly
-  // past the wave's last query is not computed (left 0, masked below)
+  // past the wave's last query is not computed (left 0, masked below).  Row
+  // lane % 32 (+ 32) of the tile, chunk 2 ks + hl.
   auto qk = [&](int buf, int kv0, f32x16 (&st)[2]) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
-    const uint16_t* kp = Ks[buf] + (lane & 31) * AP_LDK + hl * 8;
+    const uint8_t* kp = smem + buf * AP_TILE + (lane & 31) * AP_ROWB;
     if (kv0 + 32 <= wave_last) {
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ks * 16);
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kp + 32 * AP_LDK + ks * 16);
+        const int so = ap_kslot(lane, 2 * ks + hl) * 16;
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + so);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kp + 32 * AP_ROWB + so);
         st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
         st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], st[1], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ks * 16);
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ap_kslot(lane, 2 * ks + hl) * 16);
         st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
       }
     }
   };
-  // softmax of the tile at kv0 and O^T += V^T P^T (V^T of this tile in LDS)
-  auto softmax_pv = [&](int kv0, f32x16 (&st)[2]) {
+
+  // V^T fragments.  MFMA s of O^T += V^T P^T takes keys 16s..16s+15 in the
+  // order of the P^T registers: element jj of lane l (hl = l / 32) is key
+  // 16s + 8 (jj / 4) + 4 hl + jj % 4, and the A operand of lane l is dim
+  // 32 db + l % 32 at those keys.  Two transposing reads give it: read rd
+  // (keys 16s + 8 rd + 4 hl + [0, 4)) has lane l of 16-lane group g point at
+  // row 16s + 8 rd + 4 (g / 2) + e (e = (l / 4) % 4), dims
+  // 32 db + 16 (g % 2) + 4 (l % 4) + [0, 4): chunk 4 db + 2 (g % 2) + (l % 4) / 2,
+  // byte 8 ((l % 4) % 2) in it.  With r % 4 == e the slot is
+  // 4 (db ^ e) + ((2 (g % 2) + (l % 4) / 2) ^ 2 (e / 2)).
+  const int vg = lane >> 4, ve = (lane >> 2) & 3, vq = lane & 3;
+  const uint32_t vlane = uint32_t((4 * (vg >> 1) + ve) * AP_ROWB +
+                                  (((2 * (vg & 1) + (vq >> 1)) ^ (2 * (ve >> 1))) * 16) + 8 * (vq & 1));
+  uint32_t vdb[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) vdb[db] = vlane + uint32_t(64 * (db ^ ve));
+
+  // softmax of the tile at kv0 and O^T += V^T P^T (V of this tile in buffer buf)
+  auto softmax_pv = [&](int buf, int kv0, f32x16 (&st)[2]) {
     const bool live1 = kv0 + 32 <= wave_last;
     // causal / range mask only where a tile reaches past the wave's first query
     if (kv0 + AP_KT - 1 > wave_first || kv0 + AP_KT > kv_end) {
@@ -457,67 +467,78 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
       m_run = m_new;
     }
     // p = 2^(s * scale - m) in one FMA + v_exp (masked s = -inf gives 0); a
-    // lane with no visible key yet keeps m_run = -inf and every s = -inf
+    // lane with no visible key yet keeps m_run = -inf and every s = -inf.
+    // The row sum adds the fp32 p; P goes to bf16 pairs (the MFMA's B operand).
     const float mb = m_run == -INFINITY ? 0.0f : m_run;
+    uint32_t pk[2][8];
+    float l0 = 0.0f, l1 = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[kb][i], scale_log2, -mb));
-        st[kb][i] = p;
-        l_run += p;
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kb][2 * i], scale_log2, -mb));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kb][2 * i + 1], scale_log2, -mb));
+        const bf16x2_t pp = {static_cast<__bf16>(p0), static_cast<__bf16>(p1)};
+        pk[kb][i] = __builtin_bit_cast(uint32_t, pp);
+        l0 += p0;
+        l1 += p1;
       }
+    l_run += l0 + l1;
     // O^T += V^T P^T over 4 steps of 16 keys (the last two only for live keys 32..63)
+    const uint8_t* vb = smem + (2 + buf) * AP_TILE;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s >= 2 && !live1) break;
-      bf16x8 pb;
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) pb[jj] = static_cast<__bf16>(st[s >> 1][(s & 1) * 8 + jj]);
+      const u32x4 pw = {pk[s >> 1][(s & 1) * 4], pk[s >> 1][(s & 1) * 4 + 1], pk[s >> 1][(s & 1) * 4 + 2],
+                        pk[s >> 1][(s & 1) * 4 + 3]};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const bf16x8 a =
-            *reinterpret_cast<const bf16x8*>(Vt + (db * 32 + (lane & 31)) * AP_LDV + s * 16 + hl * 8);
+        const s16x4 v0 = lds_read_tr16(vb + vdb[db] + (16 * s) * AP_ROWB);
+        const s16x4 v1 = lds_read_tr16(vb + vdb[db] + (16 * s + 8) * AP_ROWB);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, o[db], 0, 0, 0);
       }
     }
   };
 
+  // Prologue: K(0), V(0), K(1), V(1) in flight; wait for the first three.
+  dma_k(0, 0);
+  dma_v(0, 0);
+  if (n_kt > 1) {
+    dma_k(1, 1);
+    dma_v(1, 1);
+    pipe::wait_vm<4>();
+  } else {
+    pipe::wait_vm<0>();
+  }
+  __syncthreads();  // K(0), V(0), K(1) visible
   f32x16 sc[2], sn[2];
-  if (n_kt > 0) {
-    gload_k(0);
-    gload_v(0);
-    lstore_k(0);
-    lstore_v();
-    if (n_kt > 1) {
-      gload_k(1);
-      gload_v(1);
-    }
-    __syncthreads();  // K(0), V(0) visible
-    if (0 <= wave_last) qk(0, 0, sc);
-    if (n_kt > 1) lstore_k(1);
-    if (n_kt > 2) gload_k(2);
+  qk(0, 0, sc);  // wave_last >= 0: tile 0 always holds visible keys
+  if (n_kt > 2) {
+    __syncthreads();  // every wave is done with K(0)'s buffer
+    dma_k(2, 0);
   }
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int kv0 = kt * AP_KT;
-    __syncthreads();  // A: K(kt+1), V(kt) visible; K(kt)'s buffer is free
-    const bool next_live = kt + 1 < n_kt && kv0 + AP_KT <= wave_last;
-    if (next_live) qk((kt + 1) & 1, kv0 + AP_KT, sn);
-    if (kv0 <= wave_last) softmax_pv(kv0, sc);  // past this wave's queries: nothing (wave-uniform)
-    if (kt + 2 < n_kt) {
-      lstore_k(kt & 1);
-      if (kt + 3 < n_kt) gload_k(kt + 3);
-    }
-    __syncthreads();  // B: every wave is done reading V(kt)
-    if (kt + 1 < n_kt) {
-      lstore_v();
-      if (kt + 2 < n_kt) gload_v(kt + 2);
-    }
-    if (next_live) {
-      sc[0] = sn[0];
-      sc[1] = sn[1];
-    }
+  // Steps in pairs, the score registers swapping roles (no copy of the next
+  // tile's scores).  Step kt: the next tile's S^T into nxt, this tile's
+  // softmax and O^T; then K(kt+2) and V(kt+1), issued after the previous
+  // barrier, have landed, and the barrier makes them visible and frees
+  // K(kt+1)'s and V(kt)'s buffers.
+  auto one = [&](int kt, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    const int kv0 = kt * AP_KT, buf = kt & 1;
+    if (kt + 1 < n_kt && kv0 + AP_KT <= wave_last) qk(buf ^ 1, kv0 + AP_KT, nxt);
+    if (kv0 <= wave_last) softmax_pv(buf, kv0, cur);  // past this wave's queries: nothing (wave-uniform)
+    pipe::wait_vm<0>();
+    __syncthreads();
+    if (kt + 3 < n_kt) dma_k(kt + 3, buf ^ 1);
+    if (kt + 2 < n_kt) dma_v(kt + 2, buf);
+  };
+  int kt = 0;
+  for (; kt + 1 < n_kt; kt += 2) {
+    one(kt, sc, sn);
+    one(kt + 1, sn, sc);
   }
+  if (kt < n_kt) one(kt, sc, sn);
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
@@ -873,6 +894,7 @@ extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill: bad heads");
   QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && start >= 0 && start + S <= S_max,
                "qmoe_attn_prefill: need 0 <= start and start + S <= S_max");
+  QMOE_REQUIRE(S_max <= AP_MAX_SMAX, "qmoe_attn_prefill: S_max must be <= %d", AP_MAX_SMAX);
   if (B == 0 || S == 0) return QMOE_OK;
   QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill: grid too large");
   const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
@@ -889,6 +911,7 @@ extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache
   QMOE_REQUIRE(D == HD, "qmoe_attn_prefill_at: head_dim must be 128");
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill_at: bad heads");
   QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max, "qmoe_attn_prefill_at: need S <= S_max");
+  QMOE_REQUIRE(S_max <= AP_MAX_SMAX, "qmoe_attn_prefill_at: S_max must be <= %d", AP_MAX_SMAX);
   if (B == 0 || S == 0) return QMOE_OK;
   QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill_at: grid too large");
   const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
