@@ -92,6 +92,10 @@ def test_version():
         (lambda l: l.qmoe_attn_decode(1, 1, 1, 1, 1, 64, 2, 128, 16, 0.1, 1, 1, None), "Hq / Hkv <= 16"),
         (lambda l: l.qmoe_attn_decode_bucket(1, 1, 1, 1, 1, 32, 4, 128, 16, 32, 0.1, 1, 1, None), "max_ctx <= S_max"),
         (lambda l: l.qmoe_attn_prefill_at(1, 1, 1, 1, 8, 32, 4, 128, 4, 1, 0.1, 1, None), "S <= S_max"),
+        (lambda l: l.qmoe_attn_prefill(1, 1, 1, 1, 10, 32, 4, 128, (1 << 22) + 1, 0, 0.1, 1, None),
+         "S_max must be <="),
+        (lambda l: l.qmoe_attn_prefill_at(1, 1, 1, 1, 8, 32, 4, 128, (1 << 22) + 1, 1, 0.1, 1, None),
+         "S_max must be <="),
         (lambda l: l.qmoe_gemv_rmsnorm(1, 1, 1e-6, 1, 100, 1536, 0, 1, None), "K must be"),
         (lambda l: l.qmoe_qkv_finish(1, 1, 1, 1, 1, 10, 1, 4, 5, 32, 4, 128, 10, 1e-6, 1, 1, 1, None), "B*S <= 16"),
     ],
