@@ -559,11 +559,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
 }
 
 // ====================================================================== decode
-constexpr int AD_SPLIT = 64;            // keys per workgroup (one wave: spreads the K/V stream over many CUs)
-constexpr int AD_WKEYS = 64;            // keys per wave; one partial (m, l, o) per wave
-constexpr int AD_SUBS = AD_SPLIT / AD_WKEYS;
+constexpr int AD_WKEYS = 64;            // keys per wave
+constexpr int AD_MAX_SUBS = 4;          // waves per workgroup (one merged partial per workgroup)
 constexpr int AD_MAX_G = 16;            // q heads per kv head
-constexpr int AD_VT_LD = AD_WKEYS + 8;  // V^T row stride in LDS (bf16): 144 B, 16-byte aligned rows
 constexpr int AD_VCH = AD_WKEYS * HD / 8 / 64;  // 16-byte V chunks per lane (16)
 constexpr int AD_PSTR = HD + 4;         // partial record: m, l, 2 pad, o[HD] (16-byte aligned o)
 constexpr int AD_MERGE_PF = 16;         // o values the merge requests before the max is known
@@ -573,20 +571,6 @@ constexpr int AD_MERGE_PF = 16;         // o values the merge requests before th
 // reads above the writes).
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Workgroup = (AD_SPLIT-key split, kv head, batch row); each of its
-// AD_SUBS waves owns 64 keys and all G q heads of the group and writes its
-// own partial (m, l, o), so no wave waits on another.  One wave per
-// workgroup: a batch-1 step has only ctx/64 x Hkv waves of work, and each
-// CU moves a limited number of bytes per microsecond, so the K/V reads are
-// spread over as many CUs as there are waves.  Per wave, on v_mfma_f32_32x32x16_bf16:
-//   S^T [64 keys x 32] = K [64 x 128] . Q^T [128 x 32]   (q heads in columns
-//       0..G-1; K rows loaded from the cache straight into A-operand registers)
-//   softmax over keys per column: lane l holds column l % 32, 32 keys; one
-//       exchange with lane l ^ 32
-//   O^T [128 x 32] = V^T [128 x 64] . P^T [64 x 32]   (V^T and bf16 P^T through
-//       this wave's LDS)
-// Every global load of the wave is issued first (K, V, q), so a split costs
-// one HBM round trip.
 // Query rows: blockIdx.z.  With chunk_start == nullptr each query row is a
 // batch row (cache row = query row) with ctx_len[row] keys; otherwise qpb
 // consecutive query rows share cache row row / qpb and query s = row % qpb
@@ -598,160 +582,216 @@ __device__ __forceinline__ int ad_ctx(const int32_t* ctx_len, const int32_t* chu
   return min(ctx_len[row], max_ctx);
 }
 
-__global__ __launch_bounds__(AD_SUBS * 64) void attn_decode_split_kernel(
+// Workgroup = (split of SUBS x 64 keys, kv head, query row); wave w owns the
+// split's keys [64 w, 64 w + 64) and all G q heads of the group.  Per wave,
+// on v_mfma_f32_32x32x16_bf16:
+//   S^T [64 keys x 32] = K [64 x 128] . Q^T [128 x 32]   (q heads in columns
+//       0..G-1; K rows loaded from the cache straight into A-operand registers)
+//   softmax over keys per column: lane l holds column l % 32, 32 keys; one
+//       exchange with lane l ^ 32
+//   O^T [128 x 32] = V^T [128 x 64] . P^T [64 x 32]   (P^T straight from the
+//       S^T registers, which already hold it in the B-operand layout; V goes
+//       into this wave's LDS row-major and the V^T fragments come from
+//       transposing reads in the key order of those registers)
+// Every global load of the wave is issued first (K, V, q), so a wave costs
+// one HBM round trip.  With SUBS == 1 (small batch x context: the K/V
+// stream of a batch-1 step spreads over ctx/64 x Hkv CUs) each wave writes
+// its partial (m, l, o); with SUBS > 1 the waves merge theirs through LDS
+// and the workgroup writes one, so the merge kernel reads SUBS times fewer.
+template <int SUBS>
+__global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len,
-    const int32_t* __restrict__ chunk_start, int qpb, int Hq, int Hkv, int S_max, int max_ctx, int nsub,
+    const int32_t* __restrict__ chunk_start, int qpb, int Hq, int Hkv, int S_max, int max_ctx, int nsplit,
     float scale, float* __restrict__ partial) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt[AD_SUBS][HD][AD_VT_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[AD_SUBS][AD_MAX_G][AD_WKEYS];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(1024))) uint8_t vs[SUBS][AP_TILE];  // V tile per wave (16 KB)
+  const int lane = threadIdx.x & 63;
+  const int wave = SUBS > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)) : 0;
   const int kvh = blockIdx.y, b = blockIdx.z, bc = chunk_start ? b / qpb : b;  // query row, cache row
   const int G = Hq / Hkv;
   const int ctx = ad_ctx(ctx_len, chunk_start, b, qpb, S_max, max_ctx);
-  const int sub = blockIdx.x * AD_SUBS + wave;
-  const int kw0 = sub * AD_WKEYS;
+  const int kw0 = (int(blockIdx.x) * SUBS + wave) * AD_WKEYS;
   const int nk = min(AD_WKEYS, ctx - kw0);
   const int col = lane & 31, hi = lane >> 5;
-  // partial record per (b, q head, sub): [m, l, -, -, o[0..127]]
-  float* pbase = partial + (int64_t(b) * Hq + kvh * G) * nsub * AD_PSTR + int64_t(sub) * AD_PSTR;
-  const int64_t pstride = int64_t(nsub) * AD_PSTR;  // next q head
-  if (nk <= 0) {
-    if (lane < G) {
-      pbase[lane * pstride] = -INFINITY;
-      pbase[lane * pstride + 1] = 0.0f;
+  // partial record per (b, q head, split): [m, l, -, -, o[0..127]]
+  float* pbase = partial + ((int64_t(b) * Hq + kvh * G) * nsplit + blockIdx.x) * AD_PSTR;
+  const int64_t pstride = int64_t(nsplit) * AD_PSTR;  // next q head
+  if (int(blockIdx.x) * SUBS * AD_WKEYS >= ctx) {  // no key of the split is visible (workgroup-uniform)
+    if (threadIdx.x < unsigned(G)) {
+      pbase[threadIdx.x * pstride] = -INFINITY;
+      pbase[threadIdx.x * pstride + 1] = 0.0f;
     }
     return;
   }
-  const int64_t kv_base = (int64_t(bc) * Hkv + kvh) * S_max * HD;
-  // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
-  u32x4 ka[2][HD / 16];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    const uint16_t* kp = k_cache + kv_base + int64_t(kw0 + min(mb * 32 + col, nk - 1)) * HD + hi * 8;
-#pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) ka[mb][ks] = ld16(kp + ks * 16);
-  }
-  // V: lane l owns key pair (2*(l%32), 2*(l%32)+1) and dim chunks c = l/32 + 2i
-  // (8 dims each), both rows, so the transpose into LDS below writes whole
-  // 32-bit key pairs with lanes on consecutive banks
-  u32x4 vr[2][AD_VCH / 2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const uint16_t* vp = v_cache + kv_base + int64_t(kw0 + min(2 * col + r, nk - 1)) * HD + hi * 8;
-#pragma unroll
-    for (int i = 0; i < AD_VCH / 2; ++i) vr[r][i] = ld16(vp + i * 16);
-  }
-  // Q^T as B operands: column col = q head, dims ks*16 + hi*8 (zero past G)
-  u32x4 qb[HD / 16];
-  const uint16_t* qp = q + (int64_t(b) * Hq + kvh * G + min(col, G - 1)) * HD + hi * 8;
-#pragma unroll
-  for (int ks = 0; ks < HD / 16; ++ks) qb[ks] = col < G ? ld16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
-
-  // V^T into LDS: vt[wave][d][key], one 32-bit (key pair) write per dim
-#pragma unroll
-  for (int i = 0; i < AD_VCH / 2; ++i) {
-    const int d0 = (hi + 2 * i) * 8;
-    const uint32_t a4[4] = {vr[0][i].x, vr[0][i].y, vr[0][i].z, vr[0][i].w};
-    const uint32_t b4[4] = {vr[1][i].x, vr[1][i].y, vr[1][i].z, vr[1][i].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<uint32_t*>(&vt[wave][d0 + 2 * j][2 * col]) = (a4[j] & 0xffffu) | (b4[j] << 16);
-      *reinterpret_cast<uint32_t*>(&vt[wave][d0 + 2 * j + 1][2 * col]) = (a4[j] >> 16) | (b4[j] & 0xffff0000u);
-    }
-  }
-
-  f32x16 sacc[2];
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    sacc[mb] = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks)
-      sacc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[mb][ks]),
-                                                         __builtin_bit_cast(bf16x8, qb[ks]), sacc[mb], 0,
-                                                         0, 0);
-  }
-  // element e of block mb: key mb*32 + (e/4)*8 + hi*4 + e%4, column col
-  float m = -INFINITY;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int key = mb * 32 + (e >> 2) * 8 + hi * 4 + (e & 3);
-      const float sv = key < nk ? sacc[mb][e] * scale : -INFINITY;
-      sacc[mb][e] = sv;
-      m = fmaxf(m, sv);
-    }
-  m = fmaxf(m, __shfl_xor(m, 32, 64));
-  float l = 0.0f;
-#pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float p = __expf(sacc[mb][e] - m);
-      sacc[mb][e] = p;
-      l += p;
-    }
-  l += __shfl_xor(l, 32, 64);
-  if (col < G) {  // P^T (bf16) into LDS: 4 consecutive keys per 8-byte write
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        u32x2 w;
-        w.x = pack_bf16x2(sacc[mb][e4 * 4 + 0], sacc[mb][e4 * 4 + 1]);
-        w.y = pack_bf16x2(sacc[mb][e4 * 4 + 2], sacc[mb][e4 * 4 + 3]);
-        *reinterpret_cast<u32x2*>(&pt[wave][col][mb * 32 + e4 * 8 + hi * 4]) = w;
-      }
-  }
-  wave_lds_sync();
-
+  float m = -INFINITY, l = 0.0f;
   f32x16 oacc[HD / 32];
 #pragma unroll
   for (int db = 0; db < HD / 32; ++db) oacc[db] = f32x16{};
+  if (nk > 0) {  // wave-uniform
+    const int64_t kv_base = (int64_t(bc) * Hkv + kvh) * S_max * HD;
+    // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
+    u32x4 ka[2][HD / 16];
 #pragma unroll
-  for (int ks = 0; ks < AD_WKEYS / 16; ++ks) {
-    const u32x4 pb = col < G ? *reinterpret_cast<const u32x4*>(&pt[wave][min(col, AD_MAX_G - 1)][ks * 16 + hi * 8])
-                             : u32x4{0u, 0u, 0u, 0u};
+    for (int mb = 0; mb < 2; ++mb) {
+      const uint16_t* kp = k_cache + kv_base + int64_t(kw0 + min(mb * 32 + col, nk - 1)) * HD + hi * 8;
 #pragma unroll
-    for (int db = 0; db < HD / 32; ++db) {
-      const u32x4 va = *reinterpret_cast<const u32x4*>(&vt[wave][db * 32 + col][ks * 16 + hi * 8]);
-      oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, va),
-                                                         __builtin_bit_cast(bf16x8, pb), oacc[db], 0, 0, 0);
+      for (int ks = 0; ks < HD / 16; ++ks) ka[mb][ks] = ld16(kp + ks * 16);
+    }
+    // V: chunk c = lane + 64 i is row c / 16 (key), dim chunk c % 16; rows
+    // past nk repeat the last visible key (their p is 0)
+    u32x4 vr[AD_VCH];
+#pragma unroll
+    for (int i = 0; i < AD_VCH; ++i) {
+      const int c = lane + 64 * i;
+      vr[i] = ld16(v_cache + kv_base + int64_t(kw0 + min(c >> 4, nk - 1)) * HD + (c & 15) * 8);
+    }
+    // Q^T as B operands: column col = q head, dims ks*16 + hi*8 (zero past G)
+    u32x4 qb[HD / 16];
+    const uint16_t* qp = q + (int64_t(b) * Hq + kvh * G + min(col, G - 1)) * HD + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) qb[ks] = col < G ? ld16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+
+    // V into this wave's LDS, row-major with the prefill's chunk swizzle
+    uint8_t* vb = vs[wave];
+#pragma unroll
+    for (int i = 0; i < AD_VCH; ++i) {
+      const int c = lane + 64 * i, r = c >> 4;
+      *reinterpret_cast<u32x4*>(vb + r * AP_ROWB + ap_vslot(r, c & 15) * 16) = vr[i];
+    }
+
+    f32x16 sacc[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      sacc[mb] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks)
+        sacc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[mb][ks]),
+                                                           __builtin_bit_cast(bf16x8, qb[ks]), sacc[mb], 0,
+                                                           0, 0);
+    }
+    // element e of block mb: key mb*32 + (e/4)*8 + hi*4 + e%4, column col
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = mb * 32 + (e >> 2) * 8 + hi * 4 + (e & 3);
+        const float sv = key < nk ? sacc[mb][e] * scale : -INFINITY;
+        sacc[mb][e] = sv;
+        m = fmaxf(m, sv);
+      }
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    uint32_t pk[2][8];  // P^T as bf16 pairs: the B operand, keys in accumulator order
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = __expf(sacc[mb][2 * i] - m), p1 = __expf(sacc[mb][2 * i + 1] - m);
+        l += p0 + p1;
+        const bf16x2_t pp = {static_cast<__bf16>(p0), static_cast<__bf16>(p1)};
+        pk[mb][i] = __builtin_bit_cast(uint32_t, pp);
+      }
+    l += __shfl_xor(l, 32, 64);
+    wave_lds_sync();
+
+    // O^T += V^T P^T, 16 keys per MFMA: element jj of the P^T operand of
+    // lane l is key 16s + 8 (jj / 4) + 4 (l / 32) + jj % 4, and two
+    // transposing reads give the matching V^T rows (same addressing as the
+    // prefill kernel's V^T fragments)
+    const int vg = lane >> 4, ve = (lane >> 2) & 3, vq = lane & 3;
+    const uint32_t vlane = uint32_t((4 * (vg >> 1) + ve) * AP_ROWB +
+                                    (((2 * (vg & 1) + (vq >> 1)) ^ (2 * (ve >> 1))) * 16) + 8 * (vq & 1));
+#pragma unroll
+    for (int s = 0; s < AD_WKEYS / 16; ++s) {
+      const u32x4 pw = {pk[s >> 1][(s & 1) * 4], pk[s >> 1][(s & 1) * 4 + 1], pk[s >> 1][(s & 1) * 4 + 2],
+                        pk[s >> 1][(s & 1) * 4 + 3]};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+#pragma unroll
+      for (int db = 0; db < HD / 32; ++db) {
+        const uint32_t va = vlane + uint32_t(64 * (db ^ ve));
+        const s16x4 v0 = lds_read_tr16(vb + va + (16 * s) * AP_ROWB);
+        const s16x4 v1 = lds_read_tr16(vb + va + (16 * s + 8) * AP_ROWB);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, oacc[db], 0, 0, 0);
+      }
     }
   }
   // element e of block db: d = db*32 + (e/4)*8 + hi*4 + e%4, column col = q head
-  if (col < G) {
-    float* pg = pbase + col * pstride;
-    if (hi == 0) {
-      pg[0] = m;
-      pg[1] = l;
+  if constexpr (SUBS == 1) {
+    if (col < G) {
+      float* pg = pbase + col * pstride;
+      if (hi == 0) {
+        pg[0] = m;
+        pg[1] = l;
+      }
+#pragma unroll
+      for (int db = 0; db < HD / 32; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4)
+          *reinterpret_cast<float4*>(pg + 4 + db * 32 + e4 * 8 + hi * 4) =
+              make_float4(oacc[db][e4 * 4], oacc[db][e4 * 4 + 1], oacc[db][e4 * 4 + 2], oacc[db][e4 * 4 + 3]);
     }
+  } else {
+    // Merge the waves' (m, l, o) in LDS: wave w's record of column c at
+    // float offset (w * AD_MAX_G + c) * AD_PSTR of the V area (free once
+    // every wave's O^T MFMAs have read it).
+    float* rec = reinterpret_cast<float*>(&vs[0][0]);
+    static_assert(SUBS * AD_MAX_G * AD_PSTR * 4 <= SUBS * AP_TILE, "merge records fit the V tiles");
+    __syncthreads();
+    if (col < G) {
+      float* pg = rec + (wave * AD_MAX_G + col) * AD_PSTR;
+      if (hi == 0) {
+        pg[0] = m;
+        pg[1] = l;
+      }
 #pragma unroll
-    for (int db = 0; db < HD / 32; ++db)
+      for (int db = 0; db < HD / 32; ++db)
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4)
-        *reinterpret_cast<float4*>(pg + 4 + db * 32 + e4 * 8 + hi * 4) =
-            make_float4(oacc[db][e4 * 4], oacc[db][e4 * 4 + 1], oacc[db][e4 * 4 + 2], oacc[db][e4 * 4 + 3]);
+        for (int e4 = 0; e4 < 4; ++e4)
+          *reinterpret_cast<float4*>(pg + 4 + db * 32 + e4 * 8 + hi * 4) =
+              make_float4(oacc[db][e4 * 4], oacc[db][e4 * 4 + 1], oacc[db][e4 * 4 + 2], oacc[db][e4 * 4 + 3]);
+    }
+    __syncthreads();
+    // thread t: column t / (SUBS * 64 / G) ... every (column, dim) once;
+    // waves without visible keys carry m = -inf, l = 0, o = 0 (weight 0)
+    for (int i = int(threadIdx.x); i < G * HD; i += SUBS * 64) {
+      const int c = i / HD, d = i % HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < SUBS; ++w) M = fmaxf(M, rec[(w * AD_MAX_G + c) * AD_PSTR]);
+      float L = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < SUBS; ++w) {
+        const float* r = rec + (w * AD_MAX_G + c) * AD_PSTR;
+        const float wt = r[0] == -INFINITY ? 0.0f : __expf(r[0] - M);
+        L = fmaf(wt, r[1], L);
+        O = fmaf(wt, r[4 + d], O);
+      }
+      float* pg = pbase + c * pstride;
+      if (d == 0) {
+        pg[0] = M;
+        pg[1] = L;
+      }
+      pg[4 + d] = O;
+    }
   }
 }
 
-// Merge of the partials that hold keys (ceil(ctx / AD_WKEYS) of them), in
-// chunks of HD partials: thread i reads partial i's (m, l) and its weight
+// Merge of the partials that hold keys (ceil(ctx / keys_per_split) of them),
+// in chunks of HD partials: thread i reads partial i's (m, l) and its weight
 // exp(m - M) goes to LDS; then every thread (one output dim d) adds its o[d]
 // of the chunk, eight loads in flight at a time.
 __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __restrict__ partial,
                                                                const int32_t* __restrict__ ctx_len,
                                                                const int32_t* __restrict__ chunk_start,
-                                                               int qpb, int S_max, int Hq, int max_ctx, int nsub,
-                                                               uint16_t* __restrict__ out) {
+                                                               int qpb, int S_max, int Hq, int max_ctx, int nsplit,
+                                                               int split_keys, uint16_t* __restrict__ out) {
   __shared__ float sw[HD];
   __shared__ float sred[2];
   const int bh = blockIdx.x;  // b * Hq + h
   const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
   const int ctx = ad_ctx(ctx_len, chunk_start, bh / Hq, qpb, S_max, max_ctx);
-  const int live = min(nsub, (ctx + AD_WKEYS - 1) / AD_WKEYS);
-  const float* p = partial + int64_t(bh) * nsub * AD_PSTR;
+  const int live = min(nsplit, (ctx + split_keys - 1) / split_keys);
+  const float* p = partial + int64_t(bh) * nsplit * AD_PSTR;
   // Loads that do not depend on the running max go out first: this thread's
   // (m, l) of partial d and the first AD_MERGE_PF o values of its dim.
   float mv = -INFINITY, lv = 0.0f;
@@ -922,8 +962,17 @@ extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache
 }
 
 extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t S_max) {
-  const int64_t nsub = (S_max + AD_SPLIT - 1) / AD_SPLIT * AD_SUBS;
-  return B * Hq * nsub * (D + 4);
+  const int64_t nsplit = (S_max + AD_WKEYS - 1) / AD_WKEYS;  // the most partials: one wave per split
+  return B * Hq * nsplit * (D + 4);
+}
+
+// Waves per split workgroup: four (one merged partial per 256 keys) when the
+// step has many 64-key waves, i.e. the batch x kv heads and the cache
+// capacity are both large; one otherwise.  Chosen from the cache shape, not
+// from max_ctx, so a bucket-sized launch and a full-capacity launch split
+// the keys alike and give the same bits.
+static int ad_subs(int64_t B, int64_t Hkv, int64_t S_max) {
+  return (B * Hkv >= 16 && (S_max + AD_WKEYS - 1) / AD_WKEYS * B * Hkv >= 2048) ? AD_MAX_SUBS : 1;
 }
 
 // B query rows; chunk_start / qpb as in ad_ctx (nullptr / 1: one query per batch row).
@@ -932,15 +981,21 @@ static int attn_decode_launch(const qmoe_bf16* q, const qmoe_bf16* k_cache, cons
                               int64_t Hq, int64_t Hkv, int64_t S_max, int64_t max_ctx, float scale,
                               float* partial, qmoe_bf16* out, hipStream_t s) {
   if (B == 0) return QMOE_OK;
-  const int nsplit = int((max_ctx + AD_SPLIT - 1) / AD_SPLIT);
-  const int nsub = nsplit * AD_SUBS;
-  hipLaunchKernelGGL(attn_decode_split_kernel, dim3(unsigned(nsplit), unsigned(Hkv), unsigned(B)),
-                     dim3(AD_SUBS * 64), 0, s, q, k_cache, v_cache, ctx_len, chunk_start, int(qpb), int(Hq),
-                     int(Hkv), int(S_max), int(max_ctx), nsub, scale, partial);
+  const int subs = ad_subs(chunk_start ? B / qpb : B, Hkv, S_max);
+  const int split_keys = subs * AD_WKEYS;
+  const int nsplit = int((max_ctx + split_keys - 1) / split_keys);
+  const dim3 grid{unsigned(nsplit), unsigned(Hkv), unsigned(B)};
+  if (subs == 1)
+    hipLaunchKernelGGL(attn_decode_split_kernel<1>, grid, dim3(64), 0, s, q, k_cache, v_cache, ctx_len, chunk_start,
+                       int(qpb), int(Hq), int(Hkv), int(S_max), int(max_ctx), nsplit, scale, partial);
+  else
+    hipLaunchKernelGGL(attn_decode_split_kernel<AD_MAX_SUBS>, grid, dim3(AD_MAX_SUBS * 64), 0, s, q, k_cache,
+                       v_cache, ctx_len, chunk_start, int(qpb), int(Hq), int(Hkv), int(S_max), int(max_ctx), nsplit,
+                       scale, partial);
   int rc = hip_status("qmoe_attn_decode(split)");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(unsigned(B * Hq)), dim3(HD), 0, s, partial, ctx_len,
-                     chunk_start, int(qpb), int(S_max), int(Hq), int(max_ctx), nsub, out);
+                     chunk_start, int(qpb), int(S_max), int(Hq), int(max_ctx), nsplit, split_keys, out);
   return hip_status("qmoe_attn_decode(merge)");
 }
 
