@@ -23,29 +23,33 @@
 #include "gemm.hpp"
 #include "mfma_pipe.hpp"
 #include "mfma_tile.hpp"
+#include "mfma_wide.hpp"
 
 namespace qmoe {
 
 constexpr int HD = 128;  // head_dim
 
 // ====================================================================== QKV
-// Per-(token, head) finish shared by both QKV kernels: two threads (half = 0,
-// 1; lanes l and l^1) load the head's fp32 values v (LDS or global, 16-byte
-// aligned; elements [32h, 32h+32) and their RoPE partners +64) into
-// registers: q/k heads get the RMSNorm over head_dim and RoPE, then q goes to
-// q_out and k / v to the cache row at the token's position (rejected
-// positions write nothing).
+// Per-(token, head) finish shared by the QKV kernels: PARTS threads (part =
+// 0 .. PARTS-1, consecutive lanes) each load W = 64 / PARTS of the head's
+// fp32 values v (LDS or global, 16-byte aligned: elements [W part, W part + W)
+// and their RoPE partners + 64) into registers: q/k heads get the RMSNorm
+// over head_dim and RoPE, then q goes to q_out and k / v to the cache row at
+// the token's position (rejected positions write nothing).
+template <int PARTS>
 __device__ __forceinline__ void qkv_finish_head(
-    const float* v, int half, int tok, int head, const int32_t* __restrict__ positions, int S,
+    const float* v, int part, int tok, int head, const int32_t* __restrict__ positions, int S,
     int Hq, int Hkv, int S_max, int max_pos, float eps, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cos,
     const float* __restrict__ rope_sin, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
-  float lo[32], hi[32];
+  constexpr int W = 64 / PARTS;
+  static_assert(PARTS == 2 || PARTS == 4, "two or four threads per head");
+  float lo[W], hi[W];
 #pragma unroll
-  for (int i = 0; i < 32; i += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(v + half * 32 + i);
-    const float4 c = *reinterpret_cast<const float4*>(v + 64 + half * 32 + i);
+  for (int i = 0; i < W; i += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(v + part * W + i);
+    const float4 c = *reinterpret_cast<const float4*>(v + 64 + part * W + i);
     lo[i] = a.x; lo[i + 1] = a.y; lo[i + 2] = a.z; lo[i + 3] = a.w;
     hi[i] = c.x; hi[i + 1] = c.y; hi[i + 2] = c.z; hi[i + 3] = c.w;
   }
@@ -57,15 +61,16 @@ __device__ __forceinline__ void qkv_finish_head(
     const uint16_t* nw = head < Hq ? qn_w : kn_w;
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
+    for (int i = 0; i < W; ++i) ss += lo[i] * lo[i] + hi[i] * hi[i];
     ss += __shfl_xor(ss, 1, 64);
+    if constexpr (PARTS == 4) ss += __shfl_xor(ss, 2, 64);
     const float r = rsqrtf(ss / float(HD) + eps);
-    const float* cs = rope_cos + int64_t(pos) * (HD / 2) + half * 32;
-    const float* sn = rope_sin + int64_t(pos) * (HD / 2) + half * 32;
+    const float* cs = rope_cos + int64_t(pos) * (HD / 2) + part * W;
+    const float* sn = rope_sin + int64_t(pos) * (HD / 2) + part * W;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float a = bf16_to_f32(nw[half * 32 + i]) * (lo[i] * r);
-      const float bb = bf16_to_f32(nw[64 + half * 32 + i]) * (hi[i] * r);
+    for (int i = 0; i < W; ++i) {
+      const float a = bf16_to_f32(nw[part * W + i]) * (lo[i] * r);
+      const float bb = bf16_to_f32(nw[64 + part * W + i]) * (hi[i] * r);
       const float c = cs[i], s = sn[i];
       lo[i] = a * c - bb * s;
       hi[i] = bb * c + a * s;
@@ -78,7 +83,7 @@ __device__ __forceinline__ void qkv_finish_head(
     dst = v_cache + ((int64_t(b) * Hkv + (head - Hq - Hkv)) * S_max + pos) * HD;
   }
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < W / 8; ++c) {
     u32x4 v0, v1;
     v0.x = pack_bf16x2(lo[c * 8 + 0], lo[c * 8 + 1]);
     v0.y = pack_bf16x2(lo[c * 8 + 2], lo[c * 8 + 3]);
@@ -88,8 +93,8 @@ __device__ __forceinline__ void qkv_finish_head(
     v1.y = pack_bf16x2(hi[c * 8 + 2], hi[c * 8 + 3]);
     v1.z = pack_bf16x2(hi[c * 8 + 4], hi[c * 8 + 5]);
     v1.w = pack_bf16x2(hi[c * 8 + 6], hi[c * 8 + 7]);
-    *reinterpret_cast<u32x4*>(dst + half * 32 + c * 8) = v0;
-    *reinterpret_cast<u32x4*>(dst + 64 + half * 32 + c * 8) = v1;
+    *reinterpret_cast<u32x4*>(dst + part * W + c * 8) = v0;
+    *reinterpret_cast<u32x4*>(dst + 64 + part * W + c * 8) = v1;
   }
 }
 
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(256) void qkv_norm_rope_kernel(
   const int row = t >> 1, half = t & 1;
   const int tok = m0 + row;
   if (tok >= T) return;
-  qkv_finish_head(ct + row * LDC, half, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
+  qkv_finish_head<2>(ct + row * LDC, half, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
                   kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
 }
 
@@ -238,9 +243,107 @@ __global__ __launch_bounds__(256, OCC) void qkv_pipe_kernel(
   for (int r0 = 0; r0 < P::BM; r0 += 128) {
     const int row = r0 + (t >> 1), tok = m0 + row;
     if (row < P::BM && tok < T)
-      qkv_finish_head(ct + row * LDC, t & 1, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
+      qkv_finish_head<2>(ct + row * LDC, t & 1, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
                       kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
   }
+}
+
+// Large-T QKV on the 8-wave wide pipeline (mfma_wide.hpp): a workgroup
+// computes 128 token rows x 640 weight rows (5 heads), 8 waves of 32 x 5
+// blocks over 64 tokens x 160 columns, three 48 KB stages.  At B = 8 x 1024
+// tokens that is 64 x 8 = 512 tiles, two full rounds of 256 CUs (the
+// one-head 256-row tiles of qkv_pipe_kernel make 1280 tiles at a lower rate
+// each).  The epilogue stages the fp32 accumulators one head at a time in
+// LDS ([128 tokens][128 + 4]) and finishes each (token, head) with four
+// threads (qkv_finish_head<4>), so the accumulators plus one thread's 32
+// finish values fit the register budget.
+using QkvWide = pipe::Wide<4, 5, 32, 3, 128>;
+constexpr int QW_HEADS = QkvWide::BM / HD;
+constexpr int QW_LDC = HD + 4;
+constexpr int QW_SMEM = QkvWide::SMEM > QkvWide::BN * QW_LDC * 4 ? QkvWide::SMEM : QkvWide::BN * QW_LDC * 4;
+static_assert(QkvWide::BM % HD == 0 && QW_SMEM <= 160 * 1024, "QKV wide tile");
+static_assert(QkvWide::THREADS == 4 * QkvWide::BN, "four threads per token row of a head");
+
+__global__ __launch_bounds__(QkvWide::THREADS, 1) void qkv_wide_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wqkv,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
+    const int32_t* __restrict__ positions, int T, int S, int H, int Hq, int Hkv, int S_max,
+    int max_pos, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache) {
+  using P = QkvWide;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int NH = Hq + 2 * Hkv, N = NH * HD;
+  // tile order as in gemm_wide_kernel: XCD-contiguous items, groups of 8
+  // token blocks walking every panel
+  const int gx = (N + P::BM - 1) / P::BM, gy = (T + P::BN - 1) / P::BN;
+  const int item = pipe::xcd_contiguous(int(blockIdx.x), gx * gy);
+  constexpr int GM = 8;
+  const int group = item / (GM * gx), first = group * GM, gm = min(gy - first, GM);
+  const int r = item - group * GM * gx;
+  const int m0 = (first + r % gm) * P::BN, n0 = (r / gm) * P::BM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const pipe::i32x4 ra = pipe::make_rsrc(wqkv, uint32_t(int64_t(N) * H * 2));
+  const pipe::i32x4 rb = pipe::make_rsrc(x, uint32_t(int64_t(T) * H * 2));
+  uint32_t vo[P::NDMA];
+#pragma unroll
+  for (int j = 0; j < P::NDMA; ++j) {
+    const int rr = P::dma_row(j, wave, lane);
+    const uint32_t c = P::dma_chunk(rr, lane);
+    if (j < P::AI)
+      vo[j] = n0 + rr < N ? uint32_t(int64_t(n0 + rr) * H * 2) + c : pipe::PAD;
+    else
+      vo[j] = m0 + rr < T ? uint32_t(int64_t(m0 + rr) * H * 2) + c : pipe::PAD;
+  }
+  // this wave's live 32-token blocks (none when its weight rows lie past N)
+  const int nb = n0 + P::wave_arow(wave) < N ? P::wave_blocks(wave, (min(T - m0, P::BN) + 31) / 32) : 0;
+  typename P::Acc acc;
+  P::run_dyn(nb, ra, rb, vo, H / P::BK, smem, acc, uint32_t(P::BK * 2), uint32_t(P::BK * 2));
+  float* ct = reinterpret_cast<float*>(smem);
+  const int part = threadIdx.x & 3, row = threadIdx.x >> 2;
+#pragma unroll
+  for (int th = 0; th < QW_HEADS; ++th) {
+    const int c0 = th * HD;
+    __syncthreads();  // the pipeline's (or the previous head's) LDS reads are done
+#pragma unroll
+    for (int j = 0; j < P::FN; ++j) {
+      if (j >= nb) break;
+      const int tr = P::acc_brow(wave, j, lane);
+#pragma unroll
+      for (int i = 0; i < P::FM; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = P::wave_arow(wave) + i * 32 + q * 8 + (lane >> 5) * 4 - c0;
+          if (col >= 0 && col < HD)
+            *reinterpret_cast<float4*>(ct + tr * QW_LDC + col) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        }
+    }
+    __syncthreads();
+    const int head = n0 / HD + th, tok = m0 + row;
+    if (head < NH && tok < T)
+      qkv_finish_head<4>(ct + row * QW_LDC, part, tok, head, positions, S, Hq, Hkv, S_max, max_pos, eps, qn_w,
+                         kn_w, rope_cos, rope_sin, q_out, k_cache, v_cache);
+  }
+}
+
+static int qkv_wide_launch(const uint16_t* x, const uint16_t* wqkv, const uint16_t* qn_w, const uint16_t* kn_w,
+                           const float* rope_cos, const float* rope_sin, const int32_t* positions, int64_t T,
+                           int64_t S, int64_t H, int64_t Hq, int64_t Hkv, int64_t S_max, int max_p, float eps,
+                           uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
+  static const bool attr = [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_wide_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, QW_SMEM);
+    return true;
+  }();
+  (void)attr;
+  const int64_t N = (Hq + 2 * Hkv) * HD;
+  const int64_t tiles = (T + QkvWide::BN - 1) / QkvWide::BN * ((N + QkvWide::BM - 1) / QkvWide::BM);
+  hipLaunchKernelGGL(qkv_wide_kernel, dim3(unsigned(tiles)), dim3(QkvWide::THREADS), QW_SMEM, s, x, wqkv, qn_w, kn_w,
+                     rope_cos, rope_sin, positions, int(T), int(S), int(H), int(Hq), int(Hkv), int(S_max), max_p, eps,
+                     q_out, k_cache, v_cache);
+  return hip_status("qmoe_qkv_norm_rope(wide)");
 }
 
 template <class P, int OCC>
@@ -887,6 +990,12 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                        int(Hq), int(Hkv), int(S_max), max_p, eps, q_out, k_cache, v_cache);
     return hip_status("qmoe_qkv_norm_rope(finish)");
   }
+  // 128 x 640 tiles on the wide pipeline once they fill every CU at least
+  // once (their 32-bit operand offsets need both operands below 2 GiB)
+  if ((T + QkvWide::BN - 1) / QkvWide::BN * (((Hq + 2 * Hkv) * HD + QkvWide::BM - 1) / QkvWide::BM) >= 256 &&
+      T * H * 2 < (1ll << 31) && (Hq + 2 * Hkv) * HD * H * 2 < (1ll << 31))
+    return qkv_wide_launch(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, T, S, H, Hq, Hkv, S_max,
+                           max_p, eps, q_out, k_cache, v_cache, as_stream(stream));
   if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32)) {
     // 256-row tiles once they give every CU a workgroup; below that 128-row
     // tiles, two per CU (a 640-token prompt: 200 workgroups instead of 120)

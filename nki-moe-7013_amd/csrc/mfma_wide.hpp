@@ -56,7 +56,7 @@ struct Wide {
   static constexpr int AI = BM / RPI / WAVES, BI = BN / RPI / WAVES, NDMA = AI + BI;  // per wave per stage
   static constexpr int KS = BK / 16;     // MFMA k-steps per stage
   static_assert(WA == 2 || WA == 4, "WA");
-  static_assert(FM == 2 || FM == 4, "FM");
+  static_assert(FM >= 1 && FM <= 5, "FM");
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(BN == 64 || BN == 128 || BN == 256, "BN");
   static_assert(S >= 3 && S <= 5, "stages");

@@ -489,12 +489,18 @@ def test_qkv_norm_rope(dev, attn_w, B, S, start):
     assert float(kc[:, :, :start].abs().sum()) == 0.0 and float(kc[:, :, start + S :].abs().sum()) == 0.0
 
 
-def test_qkv_norm_rope_wide_odd_heads(dev):
-    """Other head counts on the 256-row pipeline: 21 heads (7 q, 7 kv, odd)
-    and a ragged last token block (T = 5400), vs the oracle."""
-    Hq_, Hkv_, B, S, start = 7, 7, 1, 5400, 0
+# (7, 7, 1, 5400): 21 heads on the one-head 256-row pipeline (215 wide tiles
+# would not fill the GPU).  From 256 tiles of 128 tokens x 5 heads the wide
+# kernel runs: the attention shape with a ragged last token block (T = 4400),
+# 21 heads (five 640-row panels, the last holding one head) at T = 7800, and
+# 4 q / 1 kv heads (6 heads: a second panel with one live head) at T = 16500.
+@pytest.mark.parametrize("Hq_,Hkv_,B,S,start", [(7, 7, 1, 5400, 0), (32, 4, 4, 1100, 2), (7, 7, 2, 3900, 0),
+                                                (4, 1, 1, 16500, 0)])
+def test_qkv_norm_rope_wide_odd_heads(dev, Hq_, Hkv_, B, S, start):
+    """Other head counts and ragged token blocks on the large-T QKV
+    pipelines, vs the oracle."""
     announce(f"qkv_norm_rope wide Hq={Hq_} Hkv={Hkv_} T={B * S}")
-    g = torch.Generator(device=dev).manual_seed(21)
+    g = torch.Generator(device=dev).manual_seed(21 + Hq_ + S)
     wqkv = bf16_randn(((Hq_ + 2 * Hkv_) * D, H), g, dev, std=0.02)
     qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
     kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
