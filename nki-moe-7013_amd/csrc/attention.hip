@@ -25,6 +25,8 @@
 #include "mfma_tile.hpp"
 #include "mfma_wide.hpp"
 
+#include <type_traits>
+
 namespace qmoe {
 
 constexpr int HD = 128;  // head_dim
@@ -488,31 +490,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     for (int i = 0; i < 4; ++i) pipe::dma16(dst + i * 1024, voff[i] + adv, rv, 0);
   };
 
-  // S^T blocks of the tile at kv0 (in K buffer buf): keys [0,32) and [32,64)
-  // x this wave's 32 queries, the two MFMA chains interleaved; a block wholly
-  // past the wave's last query is not computed (left 0, masked below).  Row
+  // S^T blocks of the tile in K buffer buf: keys [0,32) and [32,64) x this
+  // wave's 32 queries, the two MFMA chains interleaved, both always computed
+  // (keys past the wave's last query are masked in the softmax; a partial
+  // 32-key half would make the score registers a merge of two paths, which
+  // the compiler resolves with a copy of all 32 of them on every step).  Row
   // lane % 32 (+ 32) of the tile, chunk 2 ks + hl.
-  auto qk = [&](int buf, int kv0, f32x16 (&st)[2]) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
+  auto qk = [&](int buf, f32x16 (&st)[2]) {
     const uint8_t* kp = smem + buf * AP_TILE + (lane & 31) * AP_ROWB;
-    if (kv0 + 32 <= wave_last) {
 #pragma unroll
-      for (int ks = 0; ks < HD / 16; ++ks) {
-        const int so = ap_kslot(lane, 2 * ks + hl) * 16;
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + so);
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kp + 32 * AP_ROWB + so);
-        st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
-        st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], st[1], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < HD / 16; ++ks) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + ap_kslot(lane, 2 * ks + hl) * 16);
-        st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], st[0], 0, 0, 0);
-      }
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const int so = ap_kslot(lane, 2 * ks + hl) * 16;
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kp + so);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kp + 32 * AP_ROWB + so);
+      st[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[ks], ks ? st[0] : f32x16{}, 0, 0, 0);
+      st[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[ks], ks ? st[1] : f32x16{}, 0, 0, 0);
     }
   };
 
@@ -535,8 +527,11 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   // softmax of the tile at kv0 and O^T += V^T P^T (V of this tile in buffer buf)
   auto softmax_pv = [&](int buf, int kv0, f32x16 (&st)[2]) {
     const bool live1 = kv0 + 32 <= wave_last;
-    // causal / range mask only where a tile reaches past the wave's first query
+    // causal / range mask only where a tile reaches past the wave's first
+    // query (this covers every tile with keys 32..63 past the wave's last
+    // query: live1 false)
     if (kv0 + AP_KT - 1 > wave_first || kv0 + AP_KT > kv_end) {
+      asm volatile("");  // keeps this a branch: the mask is not worth computing on every step
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -544,9 +539,6 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
           const int key = kv0 + kb * 32 + (i >> 2) * 8 + hl * 4 + (i & 3);
           if (key > q_idx || key >= kv_end) st[kb][i] = -INFINITY;
         }
-    } else if (!live1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) st[1][i] = -INFINITY;
     }
     float mloc = fmaxf(st[0][0], st[0][1]);
 #pragma unroll
@@ -617,19 +609,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   }
   __syncthreads();  // K(0), V(0), K(1) visible
   f32x16 sc[2], sn[2];
-  qk(0, 0, sc);  // wave_last >= 0: tile 0 always holds visible keys
+  qk(0, sc);
   if (n_kt > 2) {
     __syncthreads();  // every wave is done with K(0)'s buffer
     dma_k(2, 0);
   }
   // Steps in pairs, the score registers swapping roles (no copy of the next
-  // tile's scores).  Step kt: the next tile's S^T into nxt, this tile's
-  // softmax and O^T; then K(kt+2) and V(kt+1), issued after the previous
-  // barrier, have landed, and the barrier makes them visible and frees
-  // K(kt+1)'s and V(kt)'s buffers.
-  auto one = [&](int kt, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+  // tile's scores).  Step kt: the next tile's S^T into nxt (whenever there
+  // is a next tile, also past this wave's last query: the scores are then
+  // never read, and an unconditional nxt keeps its old value dead), this
+  // tile's softmax and O^T; then K(kt+2) and V(kt+1), issued after the
+  // previous barrier, have landed, and the barrier makes them visible and
+  // frees K(kt+1)'s and V(kt)'s buffers.
+  auto one = [&](int kt, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next) {
     const int kv0 = kt * AP_KT, buf = kt & 1;
-    if (kt + 1 < n_kt && kv0 + AP_KT <= wave_last) qk(buf ^ 1, kv0 + AP_KT, nxt);
+    if constexpr (decltype(has_next)::value) qk(buf ^ 1, nxt);
     if (kv0 <= wave_last) softmax_pv(buf, kv0, cur);  // past this wave's queries: nothing (wave-uniform)
     pipe::wait_vm<0>();
     __syncthreads();
@@ -637,11 +631,16 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     if (kt + 2 < n_kt) dma_v(kt + 2, buf);
   };
   int kt = 0;
-  for (; kt + 1 < n_kt; kt += 2) {
-    one(kt, sc, sn);
-    one(kt + 1, sn, sc);
+  for (; kt + 2 < n_kt; kt += 2) {
+    one(kt, sc, sn, std::true_type{});
+    one(kt + 1, sn, sc, std::true_type{});
   }
-  if (kt < n_kt) one(kt, sc, sn);
+  if (kt + 1 < n_kt) {
+    one(kt, sc, sn, std::true_type{});
+    one(kt + 1, sn, sc, std::false_type{});
+  } else {
+    one(kt, sc, sn, std::false_type{});
+  }
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
