@@ -464,6 +464,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   // wave_first is visible to every query of the wave (no mask)
   const int wave_first = start + q0 + wave * 32;
   const int wave_last = min(wave_first + 31, kv_end - 1);
+  const int lim = min(q_idx, kv_end - 1);  // keys visible to this lane's query: [0, lim]
 
   // DMA: wave w writes rows [16w, 16w + 16) of each K / V tile with four
   // instructions of 4 rows (1 KB of LDS each); lane j fills slot j % 16 of row
@@ -537,14 +538,18 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kv0 + kb * 32 + (i >> 2) * 8 + hl * 4 + (i & 3);
-          if (key > q_idx || key >= kv_end) st[kb][i] = -INFINITY;
+          if (key > lim) st[kb][i] = -INFINITY;
         }
     }
-    float mloc = fmaxf(st[0][0], st[0][1]);
+    // max as a tree (a 32-long chain of dependent max operations stalls)
+    float mx[16];
 #pragma unroll
-    for (int i = 2; i < 16; ++i) mloc = fmaxf(mloc, st[0][i]);
+    for (int i = 0; i < 16; ++i) mx[i] = fmaxf(st[0][i], st[1][i]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, st[1][i]);
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
+    float mloc = mx[0];
     {  // max with lane l ^ 32 (the other half of the same query's keys)
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
       mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
@@ -566,7 +571,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     // The row sum adds the fp32 p; P goes to bf16 pairs (the MFMA's B operand).
     const float mb = m_run == -INFINITY ? 0.0f : m_run;
     uint32_t pk[2][8];
-    float l0 = 0.0f, l1 = 0.0f;
+    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four partial row sums (short chains)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -575,10 +580,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
         const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kb][2 * i + 1], scale_log2, -mb));
         const bf16x2_t pp = {static_cast<__bf16>(p0), static_cast<__bf16>(p1)};
         pk[kb][i] = __builtin_bit_cast(uint32_t, pp);
-        l0 += p0;
-        l1 += p1;
+        ls[2 * (i & 1)] += p0;
+        ls[2 * (i & 1) + 1] += p1;
       }
-    l_run += l0 + l1;
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     // O^T += V^T P^T over 4 steps of 16 keys (the last two only for live keys 32..63)
     const uint8_t* vb = smem + (2 + buf) * AP_TILE;
 #pragma unroll
