@@ -541,15 +541,17 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
           if (key > lim) st[kb][i] = -INFINITY;
         }
     }
-    // max as a tree (a 32-long chain of dependent max operations stalls)
-    float mx[16];
+    // max as a tree of 3-input maxima (v_max3_f32): 17 instructions, 4 deep
+    float mx[11];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx[i] = fmaxf(st[0][i], st[1][i]);
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
-    float mloc = mx[0];
+    for (int g = 0; g < 11; ++g) {
+      const int a = 3 * g, b = 3 * g + 1, c = 3 * g + 2;
+      const float va = st[a >> 4][a & 15], vb = st[b >> 4][b & 15];
+      mx[g] = c < 32 ? fmaxf(fmaxf(va, vb), st[c >> 4][c & 15]) : fmaxf(va, vb);
+    }
+    const float m0 = fmaxf(fmaxf(mx[0], mx[1]), mx[2]), m1 = fmaxf(fmaxf(mx[3], mx[4]), mx[5]);
+    const float m2 = fmaxf(fmaxf(mx[6], mx[7]), mx[8]), m3 = fmaxf(mx[9], mx[10]);
+    float mloc = fmaxf(fmaxf(fmaxf(m0, m1), m2), m3);
     {  // max with lane l ^ 32 (the other half of the same query's keys)
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc), __float_as_uint(mloc), false, false);
       mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
