@@ -79,30 +79,71 @@ __device__ __forceinline__ int xcc_id() {
   return int(v & 7);
 }
 
-// Next item for a workgroup on XCD x (its own share first), or -1 when every
-// share is handed out.  Thread 0 only.
-__device__ __forceinline__ int claim_item(int32_t* ctr, int live, int x) {
-  const int q = live >> 3, r = live & 7;
-  for (int i = 0; i < 8; ++i) {
-    const int v = (x + i) & 7;
-    const int n = q + (v < r ? 1 : 0);
-    if (n == 0) continue;
-    const int j = atomicAdd(ctr + v, 1);
-    if (j < n) return v * q + min(v, r) + j;
+// The items of one launch in 8 shares: share v = [base(v), base(v) + n(v)).
+struct Queue {
+  int32_t* ctr;  // meta[META_CTR + 8 * kind], one counter per share
+  int q, r, x;   // live = 8 q + r items; x = this workgroup's XCD
+  __device__ Queue(int32_t* c, int live, int xcd) : ctr(c), q(live >> 3), r(live & 7), x(xcd) {}
+  __device__ int n(int v) const { return q + (v < r ? 1 : 0); }
+  __device__ int base(int v) const { return v * q + min(v, r); }
+};
+
+// Next item by scanning the shares, nearest first (own share, then XCD x+1,
+// ...), or -1 when all are handed out.  Wave 0 calls it (every lane gets the
+// result).  Lanes 0-7 read the 8 counters at once; lane 0 takes an item from
+// the first share with items left.  A counter only grows, so a share seen
+// exhausted stays so, and a failed take (another workgroup was faster)
+// exhausts that share: at most 8 failed rounds, and when every share is
+// empty one round of loads decides it (a take per share in turn would cost
+// 8 serial atomic round trips at the end of every launch).
+__device__ __forceinline__ int claim_scan(const Queue& qu) {
+  const int lane = threadIdx.x & 63;
+  const int v = (qu.x + lane) & 7;
+  for (int round = 0; round < 9; ++round) {
+    int left = 0;
+    if (lane < 8) left = qu.n(v) - __hip_atomic_load(qu.ctr + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long m = __ballot(lane < 8 && left > 0);
+    if (m == 0ull) return -1;
+    const int vv = (qu.x + __builtin_ctzll(m)) & 7;
+    int j = 0;
+    if (lane == 0) j = atomicAdd(qu.ctr + vv, 1);
+    j = __builtin_amdgcn_readfirstlane(j);
+    if (j < qu.n(vv)) return qu.base(vv) + j;
   }
-  return -1;
+  return -1;  // not reached: each share can fail a take at most once
 }
 
-// Item index for the whole workgroup (through LDS word 0, which no tile is
-// using between items), -1 when done.
-__device__ __forceinline__ int next_item(int32_t* ctr, int live, int x, uint8_t* smem) {
+// The whole workgroup's item (through LDS word 0, which no tile is using
+// between items), -1 when done.  `reserve` is thread 0's take of its own
+// share's next item, issued when the previous item started so that its
+// latency hid behind the tile (NO_RESERVE: none was taken).
+constexpr int NO_RESERVE = -(1 << 30);
+__device__ __forceinline__ int next_item(const Queue& qu, int reserve, uint8_t* smem) {
   int* slot = reinterpret_cast<int*>(smem);
   __syncthreads();  // the previous tile's epilogue has read its LDS
-  if (threadIdx.x == 0) slot[0] = claim_item(ctr, live, x);
+  if (threadIdx.x < 64) {
+    const int j = __builtin_amdgcn_readfirstlane(reserve);
+    const int item = (j >= 0 && j < qu.n(qu.x)) ? qu.base(qu.x) + j : claim_scan(qu);
+    if (threadIdx.x == 0) slot[0] = item;
+  }
   __syncthreads();
   const int item = slot[0];
   __syncthreads();  // every wave has it before the next tile's DMA lands
   return item;
+}
+
+// Thread 0's take of the next item of its own share (the result is read only
+// by the next next_item), while the share has more than one more item per
+// workgroup of the XCD left after `item`: a reserved item cannot move to a
+// workgroup that finishes first, so the last round is claimed on demand.
+// The kernels reserve only while a cold tile (weight streaming, at most 64
+// rows) runs: with every item cold (T = 128) this hides the take's round
+// trip (about 1 us an item, 4% of the launch); reserving during hot tiles
+// measured slower under skewed routing.
+__device__ __forceinline__ int reserve_own(const Queue& qu, int item) {
+  const int own = item - qu.base(qu.x);
+  const bool early = own >= 0 && own < qu.n(qu.x) && qu.n(qu.x) - own - 1 > int(gridDim.x >> 3);
+  return (early && threadIdx.x == 0) ? atomicAdd(qu.ctr + qu.x, 1) : NO_RESERVE;
 }
 
 __device__ __forceinline__ void finish_queue(int32_t* ctr, int32_t* done) {
@@ -239,12 +280,15 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_gateup_grouped_kernel(
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int npanels = (2 * I + PANEL - 1) / PANEL, live = meta[0] * npanels, xcd = xcc_id();
   int32_t* ctr = meta + META_CTR;
-  for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
+  const Queue qu(ctr, live, xcd);
+  for (int item = next_item(qu, NO_RESERVE, smem); item >= 0;) {
     const TileJob job = job_of(item, tiles, npanels);
+    const int reserve = job.rows <= COLD_MAX_ROWS ? reserve_own(qu, item) : NO_RESERVE;
     if (job.rows <= COLD_MAX_ROWS)
       gateup_tile<Cold>(job, x, w13, slot_token, T, H, I, act, smem);
     else
       gateup_tile<Hot>(job, x, w13, slot_token, T, H, I, act, smem);
+    item = next_item(qu, reserve, smem);
   }
   finish_queue(ctr, meta + META_DONE);
 }
@@ -256,12 +300,15 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_down_grouped_kernel(
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int npanels = H / PANEL, live = meta[0] * npanels, xcd = xcc_id();
   int32_t* ctr = meta + META_CTR + 8;
-  for (int item; (item = next_item(ctr, live, xcd, smem)) >= 0;) {
+  const Queue qu(ctr, live, xcd);
+  for (int item = next_item(qu, NO_RESERVE, smem); item >= 0;) {
     const TileJob job = job_of(item, tiles, npanels);
+    const int reserve = job.rows <= COLD_MAX_ROWS ? reserve_own(qu, item) : NO_RESERVE;
     if (job.rows <= COLD_MAX_ROWS && I % Cold::BK == 0)
       down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
     else
       down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
+    item = next_item(qu, reserve, smem);
   }
   finish_queue(ctr, meta + META_DONE + 1);
 }
