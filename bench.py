@@ -79,6 +79,12 @@ def git_sha():
         return None
 
 
+def _gemv_max_tokens():
+    from qmoe.moe import GEMV_MAX_TOKENS
+
+    return GEMV_MAX_TOKENS
+
+
 def make_layers(n_layers, dev, seed=0):
     import torch
 
@@ -1074,7 +1080,9 @@ def main():
         "roofline": {
             "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
                        "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else
-                      "MoE block (route + moe_gateup_gemv_kernel + moe_down_gemv_kernel + combine)",
+                      ("MoE block (route + moe_gateup_gemv_kernel + moe_down_mfma_kernel + combine)"
+                       if a.tokens <= _gemv_max_tokens() else
+                       "MoE block (route + permute + moe_gateup_grouped_kernel + moe_down_grouped_kernel + combine)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

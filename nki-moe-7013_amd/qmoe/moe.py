@@ -22,8 +22,10 @@ import torch
 from . import _lib, ops
 
 # Token counts at or below this use the HBM-bound GEMV experts; above it the
-# MFMA grouped GEMM.  (Each touched expert is streamed once either way.)
-GEMV_MAX_TOKENS = 64
+# MFMA grouped GEMM.  (Each touched expert is streamed once either way; with
+# 128 experts the two paths take the same time at T = 48 on MI355X: 242 us
+# per block, against 212 / 233 us at T = 32 and 270 / 248 us at T = 64.)
+GEMV_MAX_TOKENS = 48
 # Row tile of the prefill dispatch table: one 256 x 256 MFMA tile per (tile, panel).
 TILE_M = _lib.GROUPED_MAX_TILE_M
 
