@@ -614,9 +614,12 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     print(f"[bench] model: 48 layers loaded (random init) in {time.perf_counter() - t0:.1f}s",
           file=sys.stderr, flush=True)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=torch.Generator().manual_seed(0))
+    touched = None
     for w in range(2):  # warm-up (lazy allocations, graph capture)
         m.reset()
         first = m.prefill(prompt).argmax(-1)
+        if touched is None:  # distinct experts each layer's prompt tokens route to (the prefill is deterministic)
+            touched = [int(torch.unique(l.mlp.last_routing[2]).numel()) for l in m.model.layers]
         m.greedy_decode(first, 4)
         torch.cuda.synchronize()
         print(f"[bench] model: warm-up {w} done", file=sys.stderr, flush=True)
@@ -643,13 +646,20 @@ def bench_model(dev, prompt_len=640, new_tokens=256, n_layers=48):
     # part at a near-tied step (top-2 logits within ~1e-3 on this random model)
     same = (spec_out[0, prompt_len + 1:].cpu() == toks[0].cpu()).int()
     spec_prefix = int(same.cumprod(0).sum())
-    # TTFT reads every weight but the embedding table (60.44 GB of bf16) and
-    # does 3.66 TFLOP (2 x 30.2 B non-embedding params x 640 tokens, and the
-    # causal attention): memory-bound at 7.56 ms for 8 TB/s
-    ttft_bytes, ttft_flop = 60.44e9, 3.66e12
+    # TTFT reads the attention, router, norm and lm_head weights (2.46 GB of
+    # bf16) and the weights of every expert the prompt routes to in each layer
+    # (9,437,184 B each; all 128 experts of all 48 layers would make 60.44 GB),
+    # and does 3.66 TFLOP (2 x 30.2 B non-embedding params x 640 tokens, and
+    # the causal attention)
+    ttft_all_bytes, ttft_flop = 60.44e9, 3.66e12
+    ttft_bytes = ttft_all_bytes - (n_layers * E - sum(touched)) * EXPERT_BYTES
     return {
         "ttft_ms": ttft_ms,
         "ttft_hbm_frac": ttft_bytes / (ttft_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "ttft_bytes_GB": ttft_bytes / 1e9,
+        "ttft_touched_experts_per_layer": {"mean": sum(touched) / len(touched), "min": min(touched),
+                                           "max": max(touched)},
+        "ttft_hbm_frac_if_all_experts": ttft_all_bytes / (ttft_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "ttft_mfma_frac": ttft_flop / (ttft_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         "prefill_tokens_per_s": prompt_len / (ttft_ms * 1e-3),
         "decode_tokens_per_s": new_tokens / (dec_ms * 1e-3),
