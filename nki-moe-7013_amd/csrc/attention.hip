@@ -1004,14 +1004,19 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                            max_p, eps, q_out, k_cache, v_cache, as_stream(stream));
   if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32)) {
     // 256-row tiles once they give every CU a workgroup; below that 128-row
-    // tiles, two per CU (a 640-token prompt: 200 workgroups instead of 120)
+    // tiles, two per CU, while they fill the CUs; below that 64-row tiles
+    // (a 640-token prompt: 400 workgroups instead of 200)
     if ((T + 255) / 256 * (Hq + 2 * Hkv) >= 256)
       return qkv_pipe_launch<pipe::Pipe<256, 128, 64, 2>, 1>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
                                                               positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
                                                               k_cache, v_cache, as_stream(stream));
-    return qkv_pipe_launch<pipe::Pipe<128, 128, 64, 2>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
-                                                            positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
-                                                            k_cache, v_cache, as_stream(stream));
+    if ((T + 127) / 128 * (Hq + 2 * Hkv) >= 256)
+      return qkv_pipe_launch<pipe::Pipe<128, 128, 64, 2>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                              positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                              k_cache, v_cache, as_stream(stream));
+    return qkv_pipe_launch<pipe::Pipe<64, 128, 64, 3>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                           positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                           k_cache, v_cache, as_stream(stream));
   }
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + tile::BM - 1) / tile::BM));
   hipLaunchKernelGGL(qkv_norm_rope_kernel, grid, dim3(256), 0, as_stream(stream), x, wqkv, q_norm_w,

@@ -76,12 +76,12 @@ struct Pipe {
   static constexpr int SMEM = S * STAGE;
   static constexpr int AI = BM / RPI / 4, BI = BN / RPI / 4, NDMA = AI + BI;  // per wave per stage
   static constexpr int KS = BK / 16;    // MFMA k-steps per stage
-  static constexpr int PER = NDMA / KS; // DMA instructions issued per k-step
+  static constexpr int PER = (NDMA + KS - 1) / KS;  // DMA instructions issued per k-step (the last k-steps may issue fewer)
   static constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(S >= 2 && S <= 4, "stages");
   static_assert(AI * RPI * 4 == BM && BI * RPI * 4 == BN, "tile rows per DMA");
-  static_assert(NDMA % KS == 0 && FM >= 1 && FN >= 1, "shape");
+  static_assert(FM >= 1 && FN >= 1, "shape");
   static_assert(SMEM <= 160 * 1024, "LDS");
 
   typedef f32x16 Acc[FM][FN];
@@ -124,6 +124,7 @@ struct Pipe {
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
         const int j = part * PER + q;
+        if (j >= NDMA) break;
         if (j < AI)
           dma16(sb + uint32_t((wave * AI + j) * 1024), vo[j], ra, soff_a);
         else
