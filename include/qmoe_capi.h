@@ -91,6 +91,24 @@ int qmoe_router_topk(const qmoe_bf16* x, const qmoe_bf16* w_router, const float*
                      int64_t T, int64_t H, int64_t E, int64_t k, int32_t* topk_idx,
                      float* topk_w, float* logits, qmoe_stream_t stream);
 
+/* qmoe_router_topk with a caller-owned workspace of workspace_bytes (at least
+ * qmoe_router_workspace(T, H, E) to be used): for T > 16 the logits GEMM then
+ * runs split-K (its E = 128 columns give few tiles over the long K = H), the
+ * slices summed in a fixed order by the top-k launch, so results repeat
+ * bit for bit (they may differ from the unsplit call in the last bits of the
+ * logits).  A NULL or smaller workspace: the unsplit path.  Same limits.
+ * Replaces: the router of qmoe_router_topk (qwen_with_nki.py:8589-8590,
+ *   9886-9888, 9894, 2399-2405). */
+int qmoe_router_topk_ws(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias,
+                        int64_t T, int64_t H, int64_t E, int64_t k, int32_t* topk_idx,
+                        float* topk_w, float* logits, void* workspace, int64_t workspace_bytes,
+                        qmoe_stream_t stream);
+
+/* Workspace bytes qmoe_router_topk_ws / qmoe_moe_route_ws use for T tokens
+ * (0: that size never splits; -1 for bad sizes).
+ * Replaces: nothing in the reference (a sizing helper of this library). */
+int64_t qmoe_router_workspace(int64_t T, int64_t H, int64_t E);
+
 /* Expert dispatch metadata (histogram, exclusive scan, stable permutation).
  *   topk_idx: i32 [T, k]
  *   counts: i32 [E]; offsets: i32 [E+1]; slot_token: i32 [T*k] (token of each
@@ -130,6 +148,16 @@ int qmoe_moe_route(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* b
                    float* logits, int32_t* topk_idx, float* topk_w, int32_t* counts,
                    int32_t* offsets, int32_t* slot_token, int32_t* token_slot, int32_t* active,
                    int32_t* tiles, int32_t* meta, qmoe_stream_t stream);
+
+/* qmoe_moe_route with the router workspace of qmoe_router_topk_ws.
+ * Replaces: as qmoe_moe_route (qwen_with_nki.py:8589-8590, 9886-9894,
+ *   5872-5881). */
+int qmoe_moe_route_ws(const qmoe_bf16* x, const qmoe_bf16* w_router, const float* bias, int64_t T,
+                      int64_t H, int64_t E, int64_t k, int64_t tile_m, int64_t max_tiles,
+                      float* logits, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                      int32_t* offsets, int32_t* slot_token, int32_t* token_slot, int32_t* active,
+                      int32_t* tiles, int32_t* meta, void* workspace, int64_t workspace_bytes,
+                      qmoe_stream_t stream);
 
 /* The whole MoE block at decode shape (T <= 8) in three launches: router
  * logits (with the post-attention RMSNorm fused when h is given); the expert

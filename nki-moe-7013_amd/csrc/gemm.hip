@@ -525,6 +525,42 @@ static int launch_splitk(const uint16_t* A, int64_t lda, const uint16_t* B, int 
   return hip_status("qmoe_gemm_ws(reduce)");
 }
 
+int64_t gemm_splitk_bytes(int64_t M, int64_t N, int64_t K) {
+  bool small = false;
+  const int splits = (M >= 0 && N >= 0 && K >= 0) ? splitk_plan(M, N, K, &small) : 0;
+  return splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
+}
+
+int gemm_splitk_slices(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N, int64_t K,
+                       float* part, int64_t part_bytes, int* splits, hipStream_t s) {
+  bool small = false;
+  const int n = splitk_plan(M, N, K, &small);
+  *splits = 0;
+  if (n == 0 || part == nullptr || part_bytes < int64_t(n) * M * N * int64_t(sizeof(float)) ||
+      M >= (1ll << 31) || N >= (1ll << 31) || lda < K || lda % 8 != 0 ||
+      (M - 1) * lda * 2 + K * 2 >= (1ll << 31) || N * K * 2 >= (1ll << 31))
+    return QMOE_OK;
+  QMOE_REQUIRE(A && B, "gemm_splitk_slices: null pointer");
+  auto go = [&](auto tile) {
+    using P = decltype(tile);
+    static const bool attr = [] {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_splitk_kernel<P, 2>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, P::SMEM);
+      return true;
+    }();
+    (void)attr;
+    const int64_t tiles = ((M + P::BM - 1) / P::BM) * ((N + P::BN - 1) / P::BN);
+    hipLaunchKernelGGL((gemm_splitk_kernel<P, 2>), dim3(unsigned(tiles * n)), dim3(256), P::SMEM, s, A, lda, B,
+                       int(M), int(N), int(K), n, part);
+  };
+  if (small)
+    go(SplitSmall{});
+  else
+    go(SplitTiny{});
+  *splits = n;
+  return hip_status("gemm_splitk_slices");
+}
+
 // ------------------------------------------------------------------ launcher
 template <int MT, int MODE>
 static int launch_gemv_reg(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,

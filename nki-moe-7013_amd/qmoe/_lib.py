@@ -35,9 +35,13 @@ PROTOTYPES = {
     "qmoe_last_error": (c_char_p, []),
     "qmoe_rmsnorm_residual": (c_int, [P, P, P, I64, I64, c_float, P, P, P]),
     "qmoe_router_topk": (c_int, [P, P, P, I64, I64, I64, I64, P, P, P, P]),
+    "qmoe_router_topk_ws": (c_int, [P, P, P, I64, I64, I64, I64, P, P, P, P, I64, P]),
+    "qmoe_router_workspace": (c_int64, [I64, I64, I64]),
     "qmoe_moe_permute": (c_int, [P, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P]),
     "qmoe_moe_permute_tiles": (I64, [I64, I64, I64, I64]),
     "qmoe_moe_route": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P]),
+    "qmoe_moe_route_ws": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P, P, P, P, I64,
+                                  P]),
     "qmoe_moe_decode_block": (
         c_int, [P, P, P, c_float, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P, P, I64, P, P, P]),
     "qmoe_moe_decode_block_workspace": (c_int64, [I64, I64]),

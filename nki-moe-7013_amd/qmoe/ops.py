@@ -104,14 +104,25 @@ def router_topk(
     _need(topk_idx, "topk_idx", I32, (T, k))
     _need(topk_w, "topk_w", F32, (T, k))
     _same_device(x, w_router, bias, logits, topk_idx, topk_w)
+    ws = _router_workspace(T, H, E, dev)
     check(
-        lib().qmoe_router_topk(
+        lib().qmoe_router_topk_ws(
             _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, _ptr(topk_idx), _ptr(topk_w),
-            _ptr(logits), _stream(),
+            _ptr(logits), _ptr(ws), _nbytes(ws), _stream(),
         ),
-        "qmoe_router_topk",
+        "qmoe_router_topk_ws",
     )
     return logits, topk_w, topk_idx
+
+
+def _router_workspace(T: int, H: int, E: int, dev) -> Optional[torch.Tensor]:
+    """Split-K workspace of the router logits GEMM (None when T does not split)."""
+    n = int(lib().qmoe_router_workspace(T, H, E))
+    return torch.empty(max(n, 0) // 4, dtype=F32, device=dev) if n > 0 else None
+
+
+def _nbytes(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
 
 
 # ----------------------------------------------------------------- dispatch
@@ -134,6 +145,7 @@ class Route:
     logits: Optional[torch.Tensor] = None  # [T, E] f32 (filled by moe_route)
     topk_idx: Optional[torch.Tensor] = None  # [T, k] i32
     topk_w: Optional[torch.Tensor] = None  # [T, k] f32
+    router_ws: Optional[torch.Tensor] = None  # split-K partials of the router logits (T > 16)
 
     @staticmethod
     def alloc(T: int, k: int, E: int, tile_m: int, device, with_topk: bool = False) -> "Route":
@@ -147,6 +159,12 @@ class Route:
             r.topk_idx = z(T, k)
             r.topk_w = torch.empty(T, k, dtype=F32, device=device)
         return r
+
+    def ensure_router_ws(self, H: int, device) -> None:
+        """Allocate the router's split-K workspace for hidden size H (once)."""
+        need = int(lib().qmoe_router_workspace(self.T, H, self.E))
+        if need > 0 and (self.router_ws is None or _nbytes(self.router_ws) < need):
+            self.router_ws = torch.empty(need // 4, dtype=F32, device=device)
 
 
 def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Optional[Route] = None) -> Route:
@@ -181,14 +199,15 @@ def moe_route(x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[to
     if (route.T, route.k, route.E, route.tile_m) != (T, k, E, tile_m) or route.topk_idx is None:
         raise ValueError("route buffers were allocated for a different shape / without top-k buffers")
     _same_device(x, w_router, bias, route.meta)
+    route.ensure_router_ws(H, x.device)
     check(
-        lib().qmoe_moe_route(
+        lib().qmoe_moe_route_ws(
             _ptr(x), _ptr(w_router), _ptr(bias), T, H, E, k, tile_m, route.tiles.shape[0], _ptr(route.logits),
             _ptr(route.topk_idx), _ptr(route.topk_w), _ptr(route.counts), _ptr(route.offsets),
             _ptr(route.slot_token), _ptr(route.token_slot), _ptr(route.active), _ptr(route.tiles),
-            _ptr(route.meta), _stream(),
+            _ptr(route.meta), _ptr(route.router_ws), _nbytes(route.router_ws), _stream(),
         ),
-        "qmoe_moe_route",
+        "qmoe_moe_route_ws",
     )
     return route
 

@@ -179,6 +179,33 @@ def test_router_topk_shapes(dev, T, E_, H_, k, with_bias):
     np.testing.assert_allclose(tw.cpu()[ok].numpy(), rw[ok].numpy(), rtol=2e-5, atol=1e-7)
 
 
+# Split-K router logits (T > 16 with the workspace, the default of
+# ops.router_topk / moe_route) against the unsplit GEMM of qmoe_router_topk:
+# the same selection away from near-ties, logits within fp32 rounding, and the
+# same bits on a repeated call (the slices are summed in a fixed order).
+@pytest.mark.parametrize("T,H_", [(17, 2048), (640, 2048), (1000, 4096)])
+def test_router_split_k_matches_unsplit(dev, T, H_):
+    announce(f"router split-K T={T} H={H_}")
+    g = torch.Generator(device=dev).manual_seed(11 * T + H_)
+    w = bf16_randn((E, H_), g, dev, std=0.02)
+    x = bf16_randn((T, H_), g, dev)
+    assert int(_lib.lib().qmoe_router_workspace(T, H_, E)) > 0
+    l1, w1, i1 = ops.router_topk(x, w, K_TOP)
+    l2, w2, i2 = ops.router_topk(x, w, K_TOP)
+    lp = torch.empty(T, E, dtype=torch.float32, device=dev)
+    ip = torch.empty(T, K_TOP, dtype=torch.int32, device=dev)
+    wp = torch.empty(T, K_TOP, dtype=torch.float32, device=dev)
+    assert _lib.lib().qmoe_router_topk(x.data_ptr(), w.data_ptr(), None, T, H_, E, K_TOP, ip.data_ptr(),
+                                       wp.data_ptr(), lp.data_ptr(), ops._stream()) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(l1, l2) and torch.equal(i1, i2) and torch.equal(w1, w2)
+    assert float((l1 - lp).abs().max()) <= 1e-5
+    ok = gap_mask(lp.cpu(), K_TOP)
+    assert ok.float().mean() > 0.5
+    assert torch.equal(i1.cpu()[ok], ip.cpu()[ok])
+    np.testing.assert_allclose(w1.cpu()[ok].numpy(), wp.cpu()[ok].numpy(), rtol=1e-5, atol=1e-7)
+
+
 # --------------------------------------------------------------------------- permute
 # T*k <= 4096 pairs: single-workgroup kernel; above: one workgroup per
 # 1024-pair chunk (513: 5 chunks, the last ragged; 16384: 128 chunks; 40000:
