@@ -1,9 +1,9 @@
 // The whole MoE block at decode shape (T <= 8 tokens) in three launches:
 //
 //   block_logits_kernel     [optional post-attention RMSNorm] + router logits:
-//                           E single-wave workgroups, one router row each (in
-//                           registers); every wave normalises the few token
-//                           rows itself, workgroup 0 also stores them.  No
+//                           E workgroups of T waves, one router row each (in
+//                           registers); wave r normalises token row r itself,
+//                           workgroup 0 also stores the rows.  No
 //                           workgroup waits on another: cross-workgroup
 //                           counters serialise at about 20 ns per workgroup
 //                           on one address, which is what this avoids.
@@ -47,16 +47,19 @@ constexpr int BLK_RED_WAVES = 8;
 static_assert(BLK_SLICE == 8, "an item is 4 waves x 2 units");
 
 // ------------------------------------------------------------------ router logits
-// One wave per router row e.  Each lane owns H/64 positions of the token row
-// (HC chunks of 8 at c*512 + 8*lane), so the optional RMSNorm is a wave
-// reduction over registers: no LDS, no barrier, no cross-workgroup traffic.
+// One workgroup per router row e, one wave per token row (T <= 8 waves: the
+// rows' loads and reductions run side by side, not one after another).  Each
+// lane owns H/64 positions of the token row (HC chunks of 8 at c*512 + 8*lane),
+// so the optional RMSNorm is a wave reduction over registers: no LDS, no
+// barrier, no cross-workgroup traffic.  Every wave loads the router row; the
+// concurrent misses on one line merge in L2, so HBM still sees it once.
 // Workgroup 0 also stores the normalised bf16 rows for the expert kernel.
 template <int HC>
-__global__ __launch_bounds__(64) void block_logits_kernel(
+__global__ __launch_bounds__(64 * BLK_MAX_T) void block_logits_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ h, const uint16_t* __restrict__ rms_w,
     float eps, const uint16_t* __restrict__ w_router, const float* __restrict__ bias, int T, int H,
     int E, float* __restrict__ logits, uint16_t* __restrict__ x_out) {
-  const int lane = threadIdx.x, e = blockIdx.x;
+  const int lane = threadIdx.x & 63, e = blockIdx.x;
   u32x4 wr[HC], wn[HC];
 #pragma unroll
   for (int c = 0; c < HC; ++c) wr[c] = ld_stream(w_router + int64_t(e) * H + c * 512 + lane * 8);
@@ -64,7 +67,7 @@ __global__ __launch_bounds__(64) void block_logits_kernel(
   for (int c = 0; c < HC; ++c)  // the norm weights go out with the router row
     wn[c] = h ? ld16(rms_w + c * 512 + lane * 8) : u32x4{0u, 0u, 0u, 0u};
   const float b = bias ? bias[e] : 0.0f;
-  for (int r = 0; r < T; ++r) {
+  for (int r = threadIdx.x >> 6; r < T; r += blockDim.x >> 6) {
     float xf[HC][8];
     if (h) {
       float ss = 0.0f;
@@ -427,8 +430,8 @@ static int run_block(const char* fn, const qmoe_bf16* x, const float* h, const q
   switch (H / 512) {
 #define QMOE_BLK(HC)                                                                              \
   case HC:                                                                                        \
-    hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(64), 0, s, x, h, rms_w,    \
-                       eps, w_router, bias, int(T), int(H), int(E), logits, x_out);               \
+    hipLaunchKernelGGL(block_logits_kernel<HC>, dim3(unsigned(E)), dim3(unsigned(64 * T)), 0, s, x, \
+                       h, rms_w, eps, w_router, bias, int(T), int(H), int(E), logits, x_out);     \
     if (int rc = hip_status(fn)) return rc;                                                       \
     launch_block_experts<HC>(xin, logits, E, k, topk_idx, topk_w, w13, w2, T, H, I, partial, s);  \
     break;

@@ -10,6 +10,9 @@
 
 namespace qmoe {
 
+// Largest token count whose router logits run split-K.
+constexpr int64_t ROUTER_SPLIT_MAX_T = 1024;
+
 // With splits > 0 the logits are first summed from the split-K partials
 // part[slice][T][E] in slice order (fixed: the same bits every call) and
 // written to logits; then the bias is added and the top-k taken.
@@ -65,11 +68,15 @@ int router_launch(const uint16_t* x, const uint16_t* w_router, const float* bias
   } else {
     QMOE_REQUIRE(E % 128 == 0 && H % 64 == 0, "qmoe_router_topk: prefill path needs E %% 128 == 0, H %% 64 == 0");
   }
-  // T > 16: the logits GEMM has few tiles (E = 128 columns) over a long K, so
-  // with a workspace it runs split-K (the slices summed by the top-k kernel)
-  // (at most 16 slices: the top-k launch sums them from registers)
+  // 16 < T <= ROUTER_SPLIT_MAX_T: the logits GEMM has few tiles (E = 128
+  // columns) over a long K, so with a workspace it runs split-K (the slices
+  // summed by the top-k kernel; at most 16 slices, which that launch sums
+  // from registers).  Above that the unsplit GEMM already has 128 tiles at
+  // T = 4096 and the slices' extra traffic costs more than it saves
+  // (18.9 us unsplit against 21.5 us split for logits + top-k there).
   int splits = 0;
-  if (T > 16 && gemm_splitk_bytes(T, E, H) <= 16 * T * E * int64_t(sizeof(float))) {
+  if (T > 16 && T <= ROUTER_SPLIT_MAX_T &&
+      gemm_splitk_bytes(T, E, H) <= 16 * T * E * int64_t(sizeof(float))) {
     if (int rc = gemm_splitk_slices(x, H, w_router, T, E, H, static_cast<float*>(workspace), workspace_bytes,
                                     &splits, s))
       return rc;
@@ -85,7 +92,7 @@ int router_launch(const uint16_t* x, const uint16_t* w_router, const float* bias
 }
 
 int64_t router_workspace_bytes(int64_t T, int64_t H, int64_t E) {
-  const int64_t n = T > 16 ? gemm_splitk_bytes(T, E, H) : 0;
+  const int64_t n = T > 16 && T <= ROUTER_SPLIT_MAX_T ? gemm_splitk_bytes(T, E, H) : 0;
   return n <= 16 * T * E * int64_t(sizeof(float)) ? n : 0;
 }
 

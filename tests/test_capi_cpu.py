@@ -139,12 +139,14 @@ def test_router_workspace_size():
     plan of the T x E x H logits GEMM (128 x 128 tiles once there are 16 of
     them, else 64 x 64; slices double while the grid stays within 512
     workgroups and each slice keeps >= 512 / 256 columns of H), none at
-    T <= 16, and never more than 16 slices."""
+    T <= 16 or T > 1024, and never more than 16 slices."""
     l = _lib.lib()
     assert l.qmoe_router_workspace(8, 2048, 128) == 0  # GEMV path
     assert l.qmoe_router_workspace(64, 2048, 128) == 8 * 64 * 128 * 4  # 2 tiles x 8 slices
     assert l.qmoe_router_workspace(640, 2048, 128) == 8 * 640 * 128 * 4  # 20 tiles x 8
-    assert l.qmoe_router_workspace(4096, 2048, 128) == 4 * 4096 * 128 * 4  # 32 tiles of 128 x 128 x 4
+    assert l.qmoe_router_workspace(1024, 2048, 128) == 8 * 1024 * 128 * 4  # 32 tiles of 64 x 64 x 8
+    assert l.qmoe_router_workspace(1025, 2048, 128) == 0  # unsplit above 1024 tokens
+    assert l.qmoe_router_workspace(4096, 2048, 128) == 0
     assert l.qmoe_router_workspace(1000, 4096, 128) == 16 * 1000 * 128 * 4  # 32 tiles x 16
     assert l.qmoe_router_workspace(100, 192, 128) == 0  # K too short to split
     assert l.qmoe_router_workspace(-1, 2048, 128) == -1

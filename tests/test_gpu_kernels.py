@@ -183,7 +183,7 @@ def test_router_topk_shapes(dev, T, E_, H_, k, with_bias):
 # ops.router_topk / moe_route) against the unsplit GEMM of qmoe_router_topk:
 # the same selection away from near-ties, logits within fp32 rounding, and the
 # same bits on a repeated call (the slices are summed in a fixed order).
-@pytest.mark.parametrize("T,H_", [(17, 2048), (640, 2048), (1000, 4096)])
+@pytest.mark.parametrize("T,H_", [(17, 2048), (640, 2048), (1000, 4096), (1024, 2048)])
 def test_router_split_k_matches_unsplit(dev, T, H_):
     announce(f"router split-K T={T} H={H_}")
     g = torch.Generator(device=dev).manual_seed(11 * T + H_)
