@@ -371,6 +371,26 @@ int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_cache, const 
                             int64_t S_max, int64_t max_ctx, float scale, float* partial, qmoe_bf16* out,
                             qmoe_stream_t stream);
 
+/* One decode step of the attention from the raw QKV projection: the finish of
+ * qmoe_qkv_finish (q/k RMSNorm, RoPE, the new K/V row into the cache at
+ * positions[b]) and qmoe_attn_decode_bucket in one split launch + the merge,
+ * with the same result bits as those two calls.  Row b sees cache entries
+ * [0, positions[b]] (at most max_ctx of them); a position outside [0,
+ * min(S_max, max_pos)) writes nothing and gets zeros.
+ *   qkv: f32 [B, (Hq + 2*Hkv)*D] (qmoe_gemv_rmsnorm / qmoe_gemm with
+ *   QMOE_GEMM_STORE_F32); q_norm_w, k_norm_w: bf16 [D]; rope_cos, rope_sin:
+ *   f32 [max_pos, D/2]; k_cache, v_cache: bf16 [B, Hkv, S_max, D]; partial:
+ *   qmoe_attn_decode_workspace(B, Hq, D, max_ctx) floats; out: bf16 [B, Hq*D].
+ *   Limits as qmoe_attn_decode_bucket.
+ * Replaces: q_layernorm/k_layernorm, RoPE, the KV-cache update and the
+ *   token-generation attention of NeuronQwen3MoEAttention
+ *   (qwen_with_nki.py:10102-10103, 10083-10087, 9943-9946; main.py:156-161). */
+int qmoe_attn_decode_fused(const float* qkv, const qmoe_bf16* q_norm_w, const qmoe_bf16* k_norm_w,
+                           const float* rope_cos, const float* rope_sin, int64_t max_pos, const int32_t* positions,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, int64_t max_ctx,
+                           float eps, float scale, qmoe_bf16* k_cache, qmoe_bf16* v_cache, float* partial,
+                           qmoe_bf16* out, qmoe_stream_t stream);
+
 /* S consecutive queries per batch row, at cache positions start..start+S-1
  * (start: device int32[1], clamped into [0, S_max - S]); query s attends to
  * keys [0, start + s].  Computed as B*S single-query problems (the split +

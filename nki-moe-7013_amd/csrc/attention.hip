@@ -115,6 +115,18 @@ constexpr int QKV_DEC_MAX_T = 16;
 #endif
 constexpr int QKV_PIPE_MIN_T = QMOE_QKV_PIPE_MIN_T;  // token rows from which the 256-row pipeline is used
 
+// One head row of the decode finish, lane l holding elements l and l + 64
+// (its RoPE partner): RMSNorm over the 128 values (one wave reduction), the
+// norm weight, then RoPE with this position's (c, sn).  Shared by the finish
+// kernel and the fused decode attention so both give the same bits.
+__device__ __forceinline__ void finish_head(float& lo, float& hi, float wl, float wh, float c, float sn,
+                                            float eps) {
+  const float r = rsqrtf(wave_sum(lo * lo + hi * hi) / float(HD) + eps);
+  const float a = wl * (lo * r), bb = wh * (hi * r);
+  lo = a * c - bb * sn;
+  hi = bb * c + a * sn;
+}
+
 __global__ __launch_bounds__(64) void qkv_finish_kernel(
     const float* __restrict__ raw, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cos,
@@ -133,10 +145,7 @@ __global__ __launch_bounds__(64) void qkv_finish_kernel(
   uint16_t* dst;
   if (normed) {
     const float c = rope_cos[int64_t(pos) * (HD / 2) + l], sn = rope_sin[int64_t(pos) * (HD / 2) + l];
-    const float r = rsqrtf(wave_sum(lo * lo + hi * hi) / float(HD) + eps);
-    const float a = wl * (lo * r), bb = wh * (hi * r);
-    lo = a * c - bb * sn;
-    hi = bb * c + a * sn;
+    finish_head(lo, hi, wl, wh, c, sn, eps);
     if (head < Hq)
       dst = q_out + (int64_t(tok) * Hq + head) * HD;
     else
@@ -691,6 +700,31 @@ __device__ __forceinline__ int ad_ctx(const int32_t* ctx_len, const int32_t* chu
   return min(ctx_len[row], max_ctx);
 }
 
+// Fused decode (one query per batch row at positions[row]): the row sees the
+// cache entries [0, position] once its own K/V row is in, at most max_ctx of
+// them; a position outside [0, min(S_max, max_pos)) sees none (output 0).
+__device__ __forceinline__ int ad_ctx_pos(const int32_t* positions, int row, int S_max, int max_pos,
+                                          int max_ctx) {
+  const int p = positions[row];
+  return (p >= 0 && p < S_max && p < max_pos) ? min(p + 1, max_ctx) : 0;
+}
+
+// What the fused decode attention reads in place of q: the fp32 QKV
+// projection rows and the finish parameters (as qkv_finish_kernel takes
+// them), and the caches it writes each row's new K/V into.
+struct AdFinish {
+  const float* raw;  // [B][(Hq + 2 Hkv) * HD]
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  const float* cos;  // [max_pos][HD / 2]
+  const float* sin;
+  const int32_t* positions;  // [B]
+  int max_pos;
+  float eps;
+  uint16_t* k_out;  // the caches
+  uint16_t* v_out;
+};
+
 // Workgroup = (split of SUBS x 64 keys, kv head, query row); wave w owns the
 // split's keys [64 w, 64 w + 64) and all G q heads of the group.  Per wave,
 // on v_mfma_f32_32x32x16_bf16:
@@ -707,18 +741,31 @@ __device__ __forceinline__ int ad_ctx(const int32_t* ctx_len, const int32_t* chu
 // stream of a batch-1 step spreads over ctx/64 x Hkv CUs) each wave writes
 // its partial (m, l, o); with SUBS > 1 the waves merge theirs through LDS
 // and the workgroup writes one, so the merge kernel reads SUBS times fewer.
-template <int SUBS>
+//
+// FUSED: the QKV finish of the step runs here instead of in its own launch.
+// The workgroup's waves normalise and rotate the group's G q heads from the
+// fp32 projection (heads w, w + SUBS, ... per wave; finish_head, so the same
+// bits as qkv_finish_kernel) into LDS, and the one wave whose keys hold the
+// row's position p computes that row's K and V, stores them to the caches
+// for later steps and uses them in place of the cache row p it loaded (no
+// other workgroup reads row p: it lies in exactly one wave's key range).
+// The K/V stream and the score/PV MFMAs are then those of the unfused path.
+template <int SUBS, bool FUSED>
 __global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
     const uint16_t* __restrict__ v_cache, const int32_t* __restrict__ ctx_len,
     const int32_t* __restrict__ chunk_start, int qpb, int Hq, int Hkv, int S_max, int max_ctx, int nsplit,
-    float scale, float* __restrict__ partial) {
+    float scale, float* __restrict__ partial, AdFinish fin) {
   __shared__ __attribute__((aligned(1024))) uint8_t vs[SUBS][AP_TILE];  // V tile per wave (16 KB)
+  __shared__ __attribute__((aligned(16))) uint16_t qs[FUSED ? AD_MAX_G * HD : 8];  // finished q heads
+  __shared__ __attribute__((aligned(16))) uint16_t ns[FUSED ? 2 * HD : 8];         // the new K and V rows
   const int lane = threadIdx.x & 63;
   const int wave = SUBS > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6)) : 0;
   const int kvh = blockIdx.y, b = blockIdx.z, bc = chunk_start ? b / qpb : b;  // query row, cache row
   const int G = Hq / Hkv;
-  const int ctx = ad_ctx(ctx_len, chunk_start, b, qpb, S_max, max_ctx);
+  const int pos = FUSED ? fin.positions[b] : -1;
+  const int ctx = FUSED ? ad_ctx_pos(fin.positions, b, S_max, fin.max_pos, max_ctx)
+                        : ad_ctx(ctx_len, chunk_start, b, qpb, S_max, max_ctx);
   const int kw0 = (int(blockIdx.x) * SUBS + wave) * AD_WKEYS;
   const int nk = min(AD_WKEYS, ctx - kw0);
   const int col = lane & 31, hi = lane >> 5;
@@ -732,34 +779,126 @@ __global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
     }
     return;
   }
+  // FUSED: the projection values this wave finishes are requested before
+  // the K/V stream, so the finish waits for them alone
+  constexpr int HPW = FUSED ? (AD_MAX_G + SUBS - 1) / SUBS : 1;  // q heads per wave, at most
+  const bool owner = FUSED && pos < ctx && pos >= kw0 && pos < kw0 + AD_WKEYS;  // wave-uniform
+  // (the first 8 heads branch-free, heads past G loading head G - 1 again;
+  // heads 8-15 behind one test; a scheduling barrier keeps all of it ahead
+  // of the K/V requests, so the finish waits for these loads alone)
+  constexpr int HLO = (8 + SUBS - 1) / SUBS;  // per-wave share of the first 8 heads
+  float rlo[HPW], rhi[HPW], nlo[2], nhi[2], c = 0.0f, sn = 0.0f;
+  uint16_t wq[2] = {0, 0}, wk[2] = {0, 0};  // norm weights, converted where used
+  if constexpr (FUSED) {
+    const float* rq = fin.raw + (int64_t(b) * (Hq + 2 * Hkv) + kvh * G) * HD;
+#pragma unroll
+    for (int i = 0; i < HLO; ++i) {
+      const int h = min(wave + i * SUBS, G - 1);
+      rlo[i] = rq[h * HD + lane];
+      rhi[i] = rq[h * HD + lane + 64];
+    }
+    if (G > 8) {
+#pragma unroll
+      for (int i = HLO; i < HPW; ++i) {
+        const int h = min(wave + i * SUBS, G - 1);
+        rlo[i] = rq[h * HD + lane];
+        rhi[i] = rq[h * HD + lane + 64];
+      }
+    }
+    c = fin.cos[int64_t(pos) * (HD / 2) + lane];
+    sn = fin.sin[int64_t(pos) * (HD / 2) + lane];
+    wq[0] = fin.qn_w[lane];
+    wq[1] = fin.qn_w[lane + 64];
+    wk[0] = fin.kn_w[lane];
+    wk[1] = fin.kn_w[lane + 64];
+    const float* rk = fin.raw + (int64_t(b) * (Hq + 2 * Hkv) + Hq + kvh) * HD;
+    const float* rv = rk + int64_t(Hkv) * HD;
+    nlo[0] = rk[lane];
+    nhi[0] = rk[lane + 64];
+    nlo[1] = rv[lane];
+    nhi[1] = rv[lane + 64];
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float m = -INFINITY, l = 0.0f;
   f32x16 oacc[HD / 32];
 #pragma unroll
   for (int db = 0; db < HD / 32; ++db) oacc[db] = f32x16{};
-  if (nk > 0) {  // wave-uniform
-    const int64_t kv_base = (int64_t(bc) * Hkv + kvh) * S_max * HD;
-    // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
-    u32x4 ka[2][HD / 16];
+  const int64_t kv_base = (int64_t(bc) * Hkv + kvh) * S_max * HD;
+  // K rows as A operands: block mb, k-step ks: key kw0 + mb*32 + col, dims ks*16 + hi*8
+  u32x4 ka[2][HD / 16];
+  // V: chunk c = lane + 64 i is row c / 16 (key), dim chunk c % 16; rows
+  // past nk repeat the last visible key (their p is 0)
+  u32x4 vr[AD_VCH];
+  // FUSED: waves past the context load row ctx - 1 and use none of it, so the
+  // loads need no branch (one would make the finish wait for every load)
+  if (FUSED || nk > 0) {  // wave-uniform
+    const int r0 = nk > 0 ? kw0 : ctx - 1, rl = max(nk, 1) - 1;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      const uint16_t* kp = k_cache + kv_base + int64_t(kw0 + min(mb * 32 + col, nk - 1)) * HD + hi * 8;
+      const uint16_t* kp = k_cache + kv_base + int64_t(r0 + min(mb * 32 + col, rl)) * HD + hi * 8;
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) ka[mb][ks] = ld16(kp + ks * 16);
     }
-    // V: chunk c = lane + 64 i is row c / 16 (key), dim chunk c % 16; rows
-    // past nk repeat the last visible key (their p is 0)
-    u32x4 vr[AD_VCH];
 #pragma unroll
     for (int i = 0; i < AD_VCH; ++i) {
       const int c = lane + 64 * i;
-      vr[i] = ld16(v_cache + kv_base + int64_t(kw0 + min(c >> 4, nk - 1)) * HD + (c & 15) * 8);
+      vr[i] = ld16(v_cache + kv_base + int64_t(r0 + min(c >> 4, rl)) * HD + (c & 15) * 8);
     }
-    // Q^T as B operands: column col = q head, dims ks*16 + hi*8 (zero past G)
-    u32x4 qb[HD / 16];
+  }
+  // Q^T as B operands: column col = q head, dims ks*16 + hi*8 (zero past G)
+  u32x4 qb[HD / 16];
+  if constexpr (FUSED) {  // every wave, keys or not: the q heads are shared out over all of them
+    const float wl = bf16_to_f32(wq[0]), wh = bf16_to_f32(wq[1]);
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const int h = wave + i * SUBS;
+      if (h < G) {  // wave-uniform
+        finish_head(rlo[i], rhi[i], wl, wh, c, sn, fin.eps);
+        qs[h * HD + lane] = f32_to_bf16(rlo[i]);
+        qs[h * HD + lane + 64] = f32_to_bf16(rhi[i]);
+      }
+    }
+    if (owner) {
+      finish_head(nlo[0], nhi[0], bf16_to_f32(wk[0]), bf16_to_f32(wk[1]), c, sn, fin.eps);
+      const int64_t row = kv_base + int64_t(pos) * HD;
+      const uint16_t k0 = f32_to_bf16(nlo[0]), k1 = f32_to_bf16(nhi[0]);
+      const uint16_t v0 = f32_to_bf16(nlo[1]), v1 = f32_to_bf16(nhi[1]);
+      fin.k_out[row + lane] = k0;
+      fin.k_out[row + lane + 64] = k1;
+      fin.v_out[row + lane] = v0;
+      fin.v_out[row + lane + 64] = v1;
+      ns[lane] = k0;
+      ns[lane + 64] = k1;
+      ns[HD + lane] = v0;
+      ns[HD + lane + 64] = v1;
+    }
+    if constexpr (SUBS > 1)
+      __syncthreads();
+    else
+      wave_lds_sync();
+    const uint16_t* qp = qs + min(col, G - 1) * HD + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks)
+      qb[ks] = col < G ? *reinterpret_cast<const u32x4*>(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
+    if (owner) {  // row p of the cache is not written yet: take the new row
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        if (kw0 + min(mb * 32 + col, nk - 1) == pos) {
+#pragma unroll
+          for (int ks = 0; ks < HD / 16; ++ks) ka[mb][ks] = *reinterpret_cast<const u32x4*>(ns + ks * 16 + hi * 8);
+        }
+#pragma unroll
+      for (int i = 0; i < AD_VCH; ++i) {
+        const int cc = lane + 64 * i;
+        if (kw0 + min(cc >> 4, nk - 1) == pos) vr[i] = *reinterpret_cast<const u32x4*>(ns + HD + (cc & 15) * 8);
+      }
+    }
+  } else if (nk > 0) {
     const uint16_t* qp = q + (int64_t(b) * Hq + kvh * G + min(col, G - 1)) * HD + hi * 8;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qb[ks] = col < G ? ld16(qp + ks * 16) : u32x4{0u, 0u, 0u, 0u};
-
+  }
+  if (nk > 0) {  // wave-uniform
     // V into this wave's LDS, row-major with the prefill's chunk swizzle
     uint8_t* vb = vs[wave];
 #pragma unroll
@@ -889,16 +1028,20 @@ __global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
 // in chunks of HD partials: thread i reads partial i's (m, l) and its weight
 // exp(m - M) goes to LDS; then every thread (one output dim d) adds its o[d]
 // of the chunk, eight loads in flight at a time.
+// max_pos > 0: the fused decode's merge (ctx_len holds the positions).  A
+// row without visible keys gets zeros.
 __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __restrict__ partial,
                                                                const int32_t* __restrict__ ctx_len,
                                                                const int32_t* __restrict__ chunk_start,
                                                                int qpb, int S_max, int Hq, int max_ctx, int nsplit,
-                                                               int split_keys, uint16_t* __restrict__ out) {
+                                                               int split_keys, int max_pos,
+                                                               uint16_t* __restrict__ out) {
   __shared__ float sw[HD];
   __shared__ float sred[2];
   const int bh = blockIdx.x;  // b * Hq + h
   const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
-  const int ctx = ad_ctx(ctx_len, chunk_start, bh / Hq, qpb, S_max, max_ctx);
+  const int ctx = max_pos > 0 ? ad_ctx_pos(ctx_len, bh / Hq, S_max, max_pos, max_ctx)
+                              : ad_ctx(ctx_len, chunk_start, bh / Hq, qpb, S_max, max_ctx);
   const int live = min(nsplit, (ctx + split_keys - 1) / split_keys);
   const float* p = partial + int64_t(bh) * nsplit * AD_PSTR;
   // Loads that do not depend on the running max go out first: this thread's
@@ -948,7 +1091,8 @@ __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __re
   __syncthreads();
   if (lane == 0) sred[wave] = L;
   __syncthreads();
-  out[int64_t(bh) * HD + d] = f32_to_bf16(O / (sred[0] + sred[1]));
+  const float Lt = sred[0] + sred[1];
+  out[int64_t(bh) * HD + d] = f32_to_bf16(Lt > 0.0f ? O / Lt : 0.0f);
 }
 
 }  // namespace qmoe
@@ -1096,26 +1240,38 @@ static int ad_subs(int64_t B, int64_t Hkv, int64_t S_max) {
 }
 
 // B query rows; chunk_start / qpb as in ad_ctx (nullptr / 1: one query per batch row).
+// fin.raw != nullptr: the fused decode (q == nullptr, ctx_len == fin.positions).
 static int attn_decode_launch(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
                               const int32_t* ctx_len, const int32_t* chunk_start, int64_t qpb, int64_t B,
                               int64_t Hq, int64_t Hkv, int64_t S_max, int64_t max_ctx, float scale,
-                              float* partial, qmoe_bf16* out, hipStream_t s) {
+                              float* partial, qmoe_bf16* out, hipStream_t s, const AdFinish& fin = AdFinish{}) {
   if (B == 0) return QMOE_OK;
   const int subs = ad_subs(chunk_start ? B / qpb : B, Hkv, S_max);
   const int split_keys = subs * AD_WKEYS;
   const int nsplit = int((max_ctx + split_keys - 1) / split_keys);
   const dim3 grid{unsigned(nsplit), unsigned(Hkv), unsigned(B)};
-  if (subs == 1)
-    hipLaunchKernelGGL(attn_decode_split_kernel<1>, grid, dim3(64), 0, s, q, k_cache, v_cache, ctx_len, chunk_start,
-                       int(qpb), int(Hq), int(Hkv), int(S_max), int(max_ctx), nsplit, scale, partial);
-  else
-    hipLaunchKernelGGL(attn_decode_split_kernel<AD_MAX_SUBS>, grid, dim3(AD_MAX_SUBS * 64), 0, s, q, k_cache,
-                       v_cache, ctx_len, chunk_start, int(qpb), int(Hq), int(Hkv), int(S_max), int(max_ctx), nsplit,
-                       scale, partial);
+  const bool fused = fin.raw != nullptr;
+#define QMOE_AD_SPLIT(SUBS, FUSED)                                                                                 \
+  hipLaunchKernelGGL((attn_decode_split_kernel<SUBS, FUSED>), grid, dim3(SUBS * 64), 0, s, q, k_cache, v_cache,   \
+                     ctx_len, chunk_start, int(qpb), int(Hq), int(Hkv), int(S_max), int(max_ctx), nsplit, scale, \
+                     partial, fin)
+  if (subs == 1) {
+    if (fused)
+      QMOE_AD_SPLIT(1, true);
+    else
+      QMOE_AD_SPLIT(1, false);
+  } else {
+    if (fused)
+      QMOE_AD_SPLIT(AD_MAX_SUBS, true);
+    else
+      QMOE_AD_SPLIT(AD_MAX_SUBS, false);
+  }
+#undef QMOE_AD_SPLIT
   int rc = hip_status("qmoe_attn_decode(split)");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_decode_merge_kernel, dim3(unsigned(B * Hq)), dim3(HD), 0, s, partial, ctx_len,
-                     chunk_start, int(qpb), int(S_max), int(Hq), int(max_ctx), nsplit, split_keys, out);
+                     chunk_start, int(qpb), int(S_max), int(Hq), int(max_ctx), nsplit, split_keys,
+                     fused ? fin.max_pos : 0, out);
   return hip_status("qmoe_attn_decode(merge)");
 }
 
@@ -1146,6 +1302,25 @@ extern "C" int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_ca
                             as_stream(stream));
 }
 
+extern "C" int qmoe_attn_decode_fused(const float* qkv, const qmoe_bf16* q_norm_w, const qmoe_bf16* k_norm_w,
+                                      const float* rope_cos, const float* rope_sin, int64_t max_pos,
+                                      const int32_t* positions, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t S_max, int64_t max_ctx, float eps, float scale, qmoe_bf16* k_cache,
+                                      qmoe_bf16* v_cache, float* partial, qmoe_bf16* out, qmoe_stream_t stream) {
+  QMOE_REQUIRE(qkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && k_cache && v_cache && partial &&
+                   out,
+               "qmoe_attn_decode_fused: null pointer");
+  QMOE_REQUIRE(D == HD, "qmoe_attn_decode_fused: head_dim must be 128");
+  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536 && Hq + 2 * Hkv < 65536,
+               "qmoe_attn_decode_fused: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
+  QMOE_REQUIRE(B >= 0 && B < 65536 && S_max > 0 && S_max < (1ll << 30), "qmoe_attn_decode_fused: bad B/S_max");
+  QMOE_REQUIRE(max_ctx > 0 && max_ctx <= S_max, "qmoe_attn_decode_fused: need 0 < max_ctx <= S_max");
+  QMOE_REQUIRE(max_pos > 0, "qmoe_attn_decode_fused: bad max_pos");
+  AdFinish fin{qkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, int(std::min<int64_t>(max_pos, 1ll << 30)),
+               eps, k_cache, v_cache};
+  return attn_decode_launch(nullptr, k_cache, v_cache, positions, nullptr, 1, B, Hq, Hkv, S_max, max_ctx, scale,
+                            partial, out, as_stream(stream), fin);
+}
 
 extern "C" int qmoe_attn_decode_chunk(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
                                       const int32_t* start, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,

@@ -68,6 +68,8 @@ PROTOTYPES = {
     "qmoe_gemv_rmsnorm": (c_int, [P, P, c_float, P, I64, I64, c_int, P, P]),
     "qmoe_qkv_finish": (c_int, [P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, c_float, P, P, P, P]),
     "qmoe_attn_decode_bucket": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, I64, c_float, P, P, P]),
+    "qmoe_attn_decode_fused": (c_int, [P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, c_float, c_float, P, P,
+                                       P, P, P]),
     "qmoe_attn_decode_chunk": (c_int, [P, P, P, P, I64, I64, I64, I64, I64, I64, c_float, P, P, P]),
 }
 

@@ -84,6 +84,13 @@ class Attention:
         self.scale = 1.0 / math.sqrt(head_dim)
         self._ws = {}
 
+    def _decode_ws(self, B: int, cache: KVCache, device) -> torch.Tensor:
+        ws = self._ws.get((B, cache.capacity))
+        if ws is None:
+            ws = ops.attn_decode_workspace(B, self.n_q, self.head_dim, cache.capacity, device)
+            self._ws[(B, cache.capacity)] = ws
+        return ws
+
     def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
                 cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start=0,
                 ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None,
@@ -94,7 +101,10 @@ class Attention:
         S > 1: causal prefill of a chunk starting at cache index ``start`` (an
         int, or an int32 ``[1]`` device tensor for graph replays at any position).
         S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1),
-        at most ``max_ctx`` when a context bucket is given.
+        at most ``max_ctx`` when a context bucket is given.  On the GEMV path
+        (B <= 16 decode rows) the finish runs inside the attention launch
+        (``attn_decode_fused``), which sees entries ``[0, position]``: there
+        ``ctx_len`` must be ``positions + 1`` and is not read.
         ``norm = (rms_w, eps)``: ``x`` is the fp32 residual row itself (B*S == 1)
         and the input RMSNorm is fused into the QKV GEMV.
         """
@@ -103,36 +113,37 @@ class Attention:
         if qws is None:
             qws = torch.empty(max(n_ws // 4, 1), dtype=torch.float32, device=x.device)
             self._ws[("qkv", B * S)] = qws
-        if norm is not None:
-            if B * S != 1 or n_ws == 0:
-                raise ValueError("the fused input norm takes one fp32 row on the GEMV path")
-            raw = qws[: n_ws // 4].view(1, -1)
-            ops.gemv_rmsnorm(x, norm[0], norm[1], self.wqkv, _lib.GEMM_STORE_F32, out=raw)
-            q = ops.qkv_finish(raw, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S, self.n_q,
-                               self.n_kv, cache.k, cache.v, self.eps)
+        if norm is not None and (B * S != 1 or n_ws == 0):
+            raise ValueError("the fused input norm takes one fp32 row on the GEMV path")
+        if S == 1 and n_ws > 0:
+            # decode on the GEMV path: raw projection, then finish + attention in one launch
+            raw = qws[: n_ws // 4].view(B, -1)
+            if norm is not None:
+                ops.gemv_rmsnorm(x, norm[0], norm[1], self.wqkv, _lib.GEMM_STORE_F32, out=raw)
+            else:
+                ops.gemm(x, self.wqkv, _lib.GEMM_STORE_F32, out=raw)
+            o = ops.attn_decode_fused(raw, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, self.n_q,
+                                      self.n_kv, cache.k, cache.v, self.eps, self.scale,
+                                      self._decode_ws(B, cache, x.device), max_ctx=max_ctx)
         else:
             q = ops.qkv_norm_rope(x, self.wqkv, self.q_norm, self.k_norm, rope_cos, rope_sin, positions, B, S,
                                   self.n_q, self.n_kv, cache.k, cache.v, self.eps, workspace=qws)
-        if S > 1 and isinstance(start, torch.Tensor) and B * S <= CHUNK_DECODE_MAX:
-            # a few-token chunk at a device-held position (speculative verification):
-            # one decode problem per query spreads the K/V stream over many CUs
-            ws = self._ws.get(("chunk", B * S, cache.capacity))
-            if ws is None:
-                ws = ops.attn_decode_workspace(B * S, self.n_q, self.head_dim, cache.capacity, x.device)
-                self._ws[("chunk", B * S, cache.capacity)] = ws
-            o = ops.attn_decode_chunk(q.view(B * S, self.n_q, self.head_dim), cache.k, cache.v, B, S, start,
-                                      self.scale, ws)
-        elif S > 1:
-            o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
-        else:
-            if ctx_len is None:
-                ctx_len = positions + 1
-            ws = self._ws.get((B, cache.capacity))
-            if ws is None:
-                ws = ops.attn_decode_workspace(B, self.n_q, self.head_dim, cache.capacity, x.device)
-                self._ws[(B, cache.capacity)] = ws
-            o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale, ws,
-                                max_ctx=max_ctx)
+            if S > 1 and isinstance(start, torch.Tensor) and B * S <= CHUNK_DECODE_MAX:
+                # a few-token chunk at a device-held position (speculative verification):
+                # one decode problem per query spreads the K/V stream over many CUs
+                ws = self._ws.get(("chunk", B * S, cache.capacity))
+                if ws is None:
+                    ws = ops.attn_decode_workspace(B * S, self.n_q, self.head_dim, cache.capacity, x.device)
+                    self._ws[("chunk", B * S, cache.capacity)] = ws
+                o = ops.attn_decode_chunk(q.view(B * S, self.n_q, self.head_dim), cache.k, cache.v, B, S, start,
+                                          self.scale, ws)
+            elif S > 1:
+                o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
+            else:
+                if ctx_len is None:
+                    ctx_len = positions + 1
+                o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale,
+                                    self._decode_ws(B, cache, x.device), max_ctx=max_ctx)
         key = ("oproj", o.shape[0])
         if key not in self._ws:  # split-K scratch for prefill-size token counts (None: not split)
             self._ws[key] = ops.gemm_workspace(o.shape[0], self.wo.shape[0], self.wo.shape[1], x.device)

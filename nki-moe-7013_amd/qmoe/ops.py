@@ -602,6 +602,50 @@ def attn_decode_chunk(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     return out
 
 
+def attn_decode_fused(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
+                      rope_cos: torch.Tensor, rope_sin: torch.Tensor, positions: torch.Tensor, Hq: int, Hkv: int,
+                      k_cache: torch.Tensor, v_cache: torch.Tensor, eps: float, scale: Optional[float] = None,
+                      workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                      max_ctx: Optional[int] = None) -> torch.Tensor:
+    """One decode step of the attention from the raw projection ``qkv[B, (Hq+2Hkv)*D]``
+    (f32): the q/k norm + RoPE, the new K/V rows into the cache at ``positions[b]``,
+    and attention over cache entries ``[0, positions[b]]`` in one split launch and
+    the merge (``qkv_finish`` then ``attn_decode`` with ``ctx_len = positions + 1``,
+    same bits).  Returns ``[B, Hq*D]`` bf16."""
+    B = positions.shape[0]
+    D = q_norm_w.shape[0]
+    _need(qkv, "qkv", F32, (B, (Hq + 2 * Hkv) * D))
+    _need(q_norm_w, "q_norm_w", BF16, (D,))
+    _need(k_norm_w, "k_norm_w", BF16, (D,))
+    max_pos = rope_cos.shape[0]
+    _need(rope_cos, "rope_cos", F32, (max_pos, D // 2))
+    _need(rope_sin, "rope_sin", F32, (max_pos, D // 2))
+    _need(positions, "positions", I32, (B,))
+    if k_cache.dim() != 4 or k_cache.shape[:2] != (B, Hkv) or k_cache.shape[3] != D:
+        raise ValueError(f"k_cache must be [B={B}, Hkv={Hkv}, S_max, D={D}]")
+    _need(k_cache, "k_cache", BF16)
+    _need(v_cache, "v_cache", BF16, tuple(k_cache.shape))
+    S_max = k_cache.shape[2]
+    max_ctx = S_max if max_ctx is None else int(max_ctx)
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    need = int(lib().qmoe_attn_decode_workspace(B, Hq, D, max_ctx))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=F32, device=qkv.device)
+    if workspace.dtype != F32 or workspace.numel() < need or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous float32 tensor of >= {need} elements")
+    out = torch.empty(B, Hq * D, dtype=BF16, device=qkv.device) if out is None else out
+    _need(out, "out", BF16, (B, Hq * D))
+    _same_device(qkv, q_norm_w, k_norm_w, rope_cos, rope_sin, positions, k_cache, v_cache, workspace, out)
+    check(
+        lib().qmoe_attn_decode_fused(_ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cos), _ptr(rope_sin),
+                                     max_pos, _ptr(positions), B, Hq, Hkv, D, S_max, max_ctx, float(eps),
+                                     float(scale), _ptr(k_cache), _ptr(v_cache), _ptr(workspace), _ptr(out),
+                                     _stream()),
+        "qmoe_attn_decode_fused",
+    )
+    return out
+
+
 def attn_decode_workspace(B: int, Hq: int, D: int, S_max: int, device) -> torch.Tensor:
     n = int(lib().qmoe_attn_decode_workspace(B, Hq, D, S_max))
     return torch.empty(n, dtype=F32, device=device)

@@ -98,6 +98,16 @@ def test_version():
          "S_max must be <="),
         (lambda l: l.qmoe_gemv_rmsnorm(1, 1, 1e-6, 1, 100, 1536, 0, 1, None), "K must be"),
         (lambda l: l.qmoe_qkv_finish(1, 1, 1, 1, 1, 10, 1, 4, 5, 32, 4, 128, 10, 1e-6, 1, 1, 1, None), "B*S <= 16"),
+        # fused decode: qkv, q_norm_w, k_norm_w, cos, sin, max_pos, positions, B, Hq, Hkv, D, S_max, max_ctx,
+        #   eps, scale, k_cache, v_cache, partial, out, stream
+        (lambda l: l.qmoe_attn_decode_fused(1, 1, 1, 1, 1, 10, 1, 1, 32, 4, 64, 16, 16, 1e-6, 0.1, 1, 1, 1, 1, None),
+         "head_dim"),
+        (lambda l: l.qmoe_attn_decode_fused(1, 1, 1, 1, 1, 10, 1, 1, 32, 4, 128, 16, 32, 1e-6, 0.1, 1, 1, 1, 1, None),
+         "max_ctx <= S_max"),
+        (lambda l: l.qmoe_attn_decode_fused(1, 1, 1, 1, 1, 10, 1, 1, 64, 2, 128, 16, 16, 1e-6, 0.1, 1, 1, 1, 1, None),
+         "Hq / Hkv <= 16"),
+        (lambda l: l.qmoe_attn_decode_fused(None, 1, 1, 1, 1, 10, 1, 1, 32, 4, 128, 16, 16, 1e-6, 0.1, 1, 1, 1, 1,
+                                            None), "null pointer"),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(call, msg):

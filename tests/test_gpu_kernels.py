@@ -669,6 +669,65 @@ def test_qkv_finish_matches_qkv_norm_rope(dev, attn_w):
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
 
 
+# (B, Hq, Hkv, S_max, positions, bucket): the new key first in the cache, last
+# and first of a 64-key wave, G = 16 and G = 1, and 8 rows at a capacity of
+# 8193 (four waves per split workgroup, keys up to the last cache row).
+@pytest.mark.parametrize("B,Hq_,Hkv_,S_max,pos,bucket", [
+    (1, 32, 4, 2048, [0], None), (1, 32, 4, 2048, [63], 1024), (1, 32, 4, 2048, [64], 1024),
+    (3, 32, 4, 2048, [700, 5, 1023], 1024), (2, 32, 2, 512, [100, 511], None), (2, 4, 4, 512, [10, 300], None),
+    (8, 32, 4, 8193, [1279, 0, 255, 256, 4000, 8192, 63, 64], None)])
+def test_attn_decode_fused_matches_finish_then_decode(dev, B, Hq_, Hkv_, S_max, pos, bucket):
+    """qmoe_attn_decode_fused gives the bits of qmoe_qkv_finish followed by the
+    decode attention over ctx = position + 1: the same output and the same
+    cache rows written.  The cache row at each position starts as NaN, so a
+    fused launch that attended to the stale row instead of the new one fails."""
+    announce(f"attn_decode_fused B={B} Hq={Hq_} Hkv={Hkv_} S_max={S_max} pos={pos} bucket={bucket}")
+    g = torch.Generator(device=dev).manual_seed(S_max + sum(pos) + Hq_)
+    raw = torch.randn(B, (Hq_ + 2 * Hkv_) * D, generator=g, device=dev)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    cos, sin = _rope(S_max, dev)
+    kc = bf16_randn((B, Hkv_, S_max, D), g, dev)
+    vc = bf16_randn((B, Hkv_, S_max, D), g, dev)
+    for b, p in enumerate(pos):
+        kc[b, :, p] = float("nan")
+        vc[b, :, p] = float("nan")
+    pt = torch.tensor(pos, dtype=torch.int32, device=dev)
+    kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    q1 = ops.qkv_finish(raw, qn, kn, cos, sin, pt, B, 1, Hq_, Hkv_, kc1, vc1, 1e-6)
+    o1 = ops.attn_decode(q1, kc1, vc1, pt + 1, max_ctx=bucket)
+    o2 = ops.attn_decode_fused(raw, qn, kn, cos, sin, pt, Hq_, Hkv_, kc2, vc2, 1e-6, max_ctx=bucket)
+    o3 = ops.attn_decode_fused(raw, qn, kn, cos, sin, pt, Hq_, Hkv_, kc2, vc2, 1e-6, max_ctx=bucket)
+    torch.cuda.synchronize()
+    assert not torch.isnan(o1).any()
+    assert torch.equal(o2, o1) and torch.equal(o3, o1)
+    assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
+
+
+def test_attn_decode_fused_rejected_positions(dev):
+    """A position outside [0, min(S_max, max_pos)) writes no cache row and its
+    output row is zeros; the other rows are unaffected."""
+    announce("attn_decode_fused rejected positions")
+    B, S_max = 3, 256
+    g = torch.Generator(device=dev).manual_seed(5)
+    raw = torch.randn(B, (HQ + 2 * HKV) * D, generator=g, device=dev)
+    qn = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    cos, sin = _rope(S_max, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    pt = torch.tensor([-1, 17, S_max], dtype=torch.int32, device=dev)
+    kc1, vc1 = kc.clone(), vc.clone()
+    o = ops.attn_decode_fused(raw, qn, qn, cos, sin, pt, HQ, HKV, kc1, vc1, 1e-6)
+    kc2, vc2 = kc.clone(), vc.clone()
+    q = ops.qkv_finish(raw[1:2].contiguous(), qn, qn, cos, sin, pt[1:2].contiguous(), 1, 1, HQ, HKV, kc2[1:2],
+                       vc2[1:2], 1e-6)
+    ref = ops.attn_decode(q, kc2[1:2], vc2[1:2], pt[1:2] + 1)
+    torch.cuda.synchronize()
+    assert torch.equal(o[0], torch.zeros_like(o[0])) and torch.equal(o[2], torch.zeros_like(o[2]))
+    assert torch.equal(kc1[0], kc[0]) and torch.equal(kc1[2], kc[2]) and torch.equal(vc1[2], vc[2])
+    assert torch.equal(o[1:2], ref) and torch.equal(kc1[1], kc2[1]) and torch.equal(vc1[1], vc2[1])
+
+
 @pytest.mark.parametrize("ctx,bucket", [([1], 256), ([300, 1000, 17], 1024), ([256], 256),
                                         ([1000, 17, 640, 1024, 5, 900, 128, 129], 1024)])
 def test_attn_decode_bucket(dev, ctx, bucket):
