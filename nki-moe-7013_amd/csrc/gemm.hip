@@ -197,7 +197,9 @@ __global__ __launch_bounds__(256) void gemv_rms_kernel(const float* __restrict__
 // workgroup owns NB (8 or 16) output columns; wave w owns the K range
 // [w*K/4, (w+1)*K/4): its KS B operands (16 bytes of a weight row each, lane
 // l -> column l % 16, k offset (l / 16) * 8) are all loaded before A is
-// staged, the KS MFMAs accumulate, and the four waves' 16x16 partials are
+// staged (plain loads: a load touches half of each 128-byte line and the next
+// one the other half, which the nontemporal form does not keep in L1; 3-4%
+// faster), the KS MFMAs accumulate, and the four waves' 16x16 partials are
 // added in wave order through LDS.  HBM-bound like the M = 1 GEMV: the
 // arithmetic that makes dot-product GEMVs slow at M = 8 costs KS MFMAs here.
 template <int NB, int KS, int MODE>
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
     const bool live = col < NB && n0 + col < N;
     const uint16_t* bp = B + int64_t(min(n0 + col, N - 1)) * K + kw + kq * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) bw[s] = live ? ld_stream(bp + s * 32) : u32x4{0u, 0u, 0u, 0u};
+    for (int s = 0; s < KS; ++s) bw[s] = live ? ld16(bp + s * 32) : u32x4{0u, 0u, 0u, 0u};
   }
   const int kchunks = K / 8;
   stage16<256, 16>(reinterpret_cast<u32x4*>(xs), M * kchunks, [&](int c) {
@@ -599,7 +601,10 @@ template <int MODE>
 static int launch_gemv_mfma(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                             void* C, int64_t ldc, hipStream_t s) {
   const size_t shm = size_t(M) * K * 2;
-  const bool narrow = (N + 15) / 16 < 256;  // 8 columns per workgroup to fill the CUs
+  // 8 columns per workgroup unless that makes very many workgroups: at 8 rows
+  // the QKV (N = 5120, K = 2048) and o_proj (N = 2048, K = 4096) shapes run
+  // 8.7 -> 8.4 and 8.8 -> 7.9 us against 16 columns
+  const bool narrow = (N + 15) / 16 < 1024;
   static const bool attr = [] {
     for (const void* f : {reinterpret_cast<const void*>(gemv_mfma_kernel<8, 4, MODE>),
                           reinterpret_cast<const void*>(gemv_mfma_kernel<16, 4, MODE>),
