@@ -489,20 +489,30 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 using SplitSmall = pipe::Pipe<128, 128, 64, 2>;
+using SplitMid = pipe::Pipe<64, 128, 64, 3>;
 using SplitTiny = pipe::Pipe<64, 64, 64, 4>;
 
+// Tile shape of a split-K plan.
+enum SplitTile { SPLIT_TINY = 0, SPLIT_SMALL = 1, SPLIT_MID = 2 };
+
 // Split-K plan for an M > 16 problem: 0 slices = do not split (the problem
-// already has at least 256 tiles, or K is too short to split).  small = 128 x
-// 128 tiles (at least 16 of them), else 64 x 64.  Slices double while the
-// grid stays within 512 workgroups and each slice keeps >= 512 (128 x 128)
-// or >= 256 (64 x 64) columns of K, a multiple of the 64-column stage.
-static int splitk_plan(int64_t M, int64_t N, int64_t K, bool* small) {
+// already has at least 256 tiles, or K is too short to split).  Tiles: 128 x
+// 128 when there are at least 16 of them, but 64 x 128 when there are 40-127
+// (twice the tiles at half the slices: the o_proj of a 640-token prompt,
+// 640 x 2048 x 4096, runs 29.8 us as 80 tiles x 4 slices and 26.8 us as 160
+// x 2; 384 x 2048 x 4096: 21.7 -> 20.5 us), else 64 x 64.  Slices double
+// while the grid stays within 512 workgroups and each slice keeps >= 512
+// (128-column tiles) or >= 256 (64 x 64) columns of K, a multiple of the
+// 64-column stage.
+static int splitk_plan(int64_t M, int64_t N, int64_t K, SplitTile* tile) {
   if (M <= 16 || N % 4 != 0 || K % 64 != 0) return 0;
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  *small = t128 >= 16;
-  const int64_t tiles = *small ? t128 : ((M + 63) / 64) * ((N + 63) / 64);
-  const int64_t kmin = *small ? 512 : 256;
-  if (tiles >= 256) return 0;
+  *tile = t128 >= 40 && t128 < 128 ? SPLIT_MID : t128 >= 16 ? SPLIT_SMALL : SPLIT_TINY;
+  const int64_t tiles = *tile == SPLIT_SMALL ? t128
+                        : *tile == SPLIT_MID ? ((M + 63) / 64) * ((N + 127) / 128)
+                                             : ((M + 63) / 64) * ((N + 63) / 64);
+  const int64_t kmin = *tile == SPLIT_TINY ? 256 : 512;
+  if (t128 >= 256) return 0;
   int splits = 1;
   while (tiles * splits * 2 <= 512 && K % (int64_t(splits) * 2 * 64) == 0 && K / (splits * 2) >= kmin) splits *= 2;
   return splits > 1 ? splits : 0;
@@ -528,15 +538,15 @@ static int launch_splitk(const uint16_t* A, int64_t lda, const uint16_t* B, int 
 }
 
 int64_t gemm_splitk_bytes(int64_t M, int64_t N, int64_t K) {
-  bool small = false;
-  const int splits = (M >= 0 && N >= 0 && K >= 0) ? splitk_plan(M, N, K, &small) : 0;
+  SplitTile tile = SPLIT_TINY;
+  const int splits = (M >= 0 && N >= 0 && K >= 0) ? splitk_plan(M, N, K, &tile) : 0;
   return splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
 }
 
 int gemm_splitk_slices(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N, int64_t K,
                        float* part, int64_t part_bytes, int* splits, hipStream_t s) {
-  bool small = false;
-  const int n = splitk_plan(M, N, K, &small);
+  SplitTile tile = SPLIT_TINY;
+  const int n = splitk_plan(M, N, K, &tile);
   *splits = 0;
   if (n == 0 || part == nullptr || part_bytes < int64_t(n) * M * N * int64_t(sizeof(float)) ||
       M >= (1ll << 31) || N >= (1ll << 31) || lda < K || lda % 8 != 0 ||
@@ -555,8 +565,10 @@ int gemm_splitk_slices(const uint16_t* A, int64_t lda, const uint16_t* B, int64_
     hipLaunchKernelGGL((gemm_splitk_kernel<P, 2>), dim3(unsigned(tiles * n)), dim3(256), P::SMEM, s, A, lda, B,
                        int(M), int(N), int(K), n, part);
   };
-  if (small)
+  if (tile == SPLIT_SMALL)
     go(SplitSmall{});
+  else if (tile == SPLIT_MID)
+    go(SplitMid{});
   else
     go(SplitTiny{});
   *splits = n;
@@ -761,8 +773,8 @@ extern "C" int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, in
 
 extern "C" int64_t qmoe_gemm_ws_workspace(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N < 0 || K < 0) return -1;
-  bool small = false;
-  const int splits = qmoe::splitk_plan(M, N, K, &small);
+  qmoe::SplitTile tile = qmoe::SPLIT_TINY;
+  const int splits = qmoe::splitk_plan(M, N, K, &tile);
   return splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
 }
 
@@ -770,8 +782,8 @@ extern "C" int qmoe_gemm_ws(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B,
                             int64_t K, int mode, void* C, int64_t ldc, void* workspace, int64_t workspace_bytes,
                             qmoe_stream_t stream) {
   using namespace qmoe;
-  bool small = false;
-  const int splits = splitk_plan(M, N, K, &small);
+  SplitTile tile = SPLIT_TINY;
+  const int splits = splitk_plan(M, N, K, &tile);
   const int64_t need = splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
   if (splits == 0 || workspace == nullptr || workspace_bytes < need || M >= (1ll << 31) || N >= (1ll << 31))
     return gemm_launch(A, lda, B, M, N, K, mode, C, ldc, as_stream(stream));
@@ -782,9 +794,13 @@ extern "C" int qmoe_gemm_ws(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B,
                "qmoe_gemm_ws: A or B larger than 2 GiB");
   hipStream_t s = as_stream(stream);
   float* part = static_cast<float*>(workspace);
-#define QMOE_SPLIT(MODE)                                                                                 \
-  return small ? launch_splitk<SplitSmall, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C, ldc, s) \
-               : launch_splitk<SplitTiny, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C, ldc, s);
+#define QMOE_SPLIT(MODE)                                                                                    \
+  return tile == SPLIT_SMALL ? launch_splitk<SplitSmall, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C, \
+                                                               ldc, s)                                            \
+         : tile == SPLIT_MID ? launch_splitk<SplitMid, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C,   \
+                                                             ldc, s)                                              \
+                             : launch_splitk<SplitTiny, MODE>(A, lda, B, int(M), int(N), int(K), splits, part, C,  \
+                                                              ldc, s);
   switch (mode) {
     case QMOE_GEMM_STORE_BF16:
       QMOE_SPLIT(QMOE_GEMM_STORE_BF16)

@@ -162,6 +162,20 @@ def test_router_workspace_size():
     assert l.qmoe_router_workspace(-1, 2048, 128) == -1
 
 
+def test_gemm_splitk_workspace_size():
+    """Split-K workspace of qmoe_gemm_ws, f32 [slices][M][N]: 64 x 128 tiles
+    when 40-127 tiles of 128 x 128 would cover the output (640 x 2048: 160
+    tiles x 2 slices; 384 x 2048: 96 x 4), 128 x 128 from 16 such tiles
+    otherwise (1024 x 2048: 128 x 4; 256 x 2048: 32 x 8), none from 256."""
+    l = _lib.lib()
+    assert l.qmoe_gemm_ws_workspace(640, 2048, 4096) == 2 * 640 * 2048 * 4
+    assert l.qmoe_gemm_ws_workspace(384, 2048, 4096) == 4 * 384 * 2048 * 4
+    assert l.qmoe_gemm_ws_workspace(1024, 2048, 4096) == 4 * 1024 * 2048 * 4
+    assert l.qmoe_gemm_ws_workspace(256, 2048, 4096) == 8 * 256 * 2048 * 4
+    assert l.qmoe_gemm_ws_workspace(4096, 2048, 4096) == 0
+    assert l.qmoe_gemm_ws_workspace(-1, 2048, 4096) == -1
+
+
 def test_permute_tiles_rows():
     """Rows of `tiles` for the per-chunk permutation: the tile-table bound
     ceil(T*k/tile_m) + E, then (E + 1) ints of scratch per 1024-pair chunk

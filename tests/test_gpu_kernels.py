@@ -61,7 +61,10 @@ def test_gemm_vs_fp32(dev, M, N, K):
     assert float(((cbf.float().cpu() - ref).abs() - ref.abs() * 2 ** -8).max()) <= 1e-4 * scale
 
 
-@pytest.mark.parametrize("M,N,K", [(640, 2048, 4096), (640, 128, 2048), (300, 200, 1024), (1000, 512, 2048)])
+# 64 x 128 tiles (640 and 333 rows of the o_proj shape), 64 x 64 (the router
+# shape, 300 x 200), 128 x 128 (1000 x 512)
+@pytest.mark.parametrize("M,N,K", [(640, 2048, 4096), (333, 2048, 4096), (640, 128, 2048), (300, 200, 1024),
+                                   (1000, 512, 2048)])
 def test_gemm_splitk_vs_fp32(dev, M, N, K):
     """qmoe_gemm_ws: K split into slices through the workspace (the prefill
     o_proj and router shapes), each mode vs fp32; repeats are bit-identical
