@@ -38,7 +38,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Qwen3-30B-A3B-shape decode tokens/s & MoE-block GB/s (% of HBM peak)"
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0
+BF16_PEAK_TFLOPS = 2517.0  # 256 CU x 2.4 GHz x 4096 flop/clk (dense)
 H, E, I, K_TOP = 2048, 128, 768, 8
 EXPERT_BYTES = 3 * H * I * 2  # 9,437,184
 ROUTER_BYTES = E * H * 2
@@ -72,10 +72,19 @@ def parse():
 
 
 def git_sha():
+    """The commit measured: git when the tree has .git, else the commit the
+    library was built from (recorded by the build next to libqmoe.so, with a
+    +dirty suffix when the build tree had uncommitted changes)."""
     try:
         return subprocess.check_output(["git", "rev-parse", "--short", "HEAD"], cwd=ROOT,
                                        stderr=subprocess.DEVNULL).decode().strip()
     except Exception:
+        pass
+    try:
+        with open(os.path.join(ROOT, "nki-moe-7013_amd", "qmoe", "build_info.json")) as f:
+            info = json.load(f)
+        return (info["git"] + ("+dirty" if info.get("dirty") else "")) if info.get("git") else None
+    except (OSError, ValueError, KeyError):
         return None
 
 
@@ -1088,7 +1097,8 @@ def main():
         "model_prefill_tokens_per_s": round(md["prefill_tokens_per_s"], 1) if "prefill_tokens_per_s" in md else None,
         "throughputs": tp,
         "roofline": {
-            "kernel": ("qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
+            "kernel": ("qmoe_moe_decode_block: block_fused_kernel (one launch)" if a.tokens == 1 else
+                       "qmoe_moe_decode_block: block_logits_kernel + block_expert_kernel + "
                        "block_reduce_kernel (one call, 3 launches)") if a.tokens <= 8 else
                       ("MoE block (route + moe_gateup_gemv_kernel + moe_down_mfma_kernel + combine)"
                        if a.tokens <= _gemv_max_tokens() else

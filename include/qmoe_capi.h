@@ -62,8 +62,21 @@ typedef void* qmoe_stream_t;
 #define QMOE_DECODE_BLOCK_WGS 256
 
 /* Largest T * H qmoe_moe_decode_block_noalloc accepts (its static scratch is
- * QMOE_DECODE_BLOCK_WGS * this many floats = 16 MiB per GPU). */
+ * QMOE_DECODE_BLOCK_STATE_BYTES + QMOE_DECODE_BLOCK_WGS * this many floats,
+ * 16.25 MiB per GPU). */
 #define QMOE_DECODE_BLOCK_NOALLOC_MAX_TH 16384
+
+/* Bytes at the start of a decode-block workspace that carry state from one
+ * call to the next (the single-launch T = 1 path's call counters and
+ * exchange slots); the per-workgroup partials follow them.  The status word
+ * (u32) of that state sits at QMOE_DECODE_BLOCK_STATUS_OFFSET. */
+#define QMOE_DECODE_BLOCK_STATE_BYTES 262144
+#define QMOE_DECODE_BLOCK_STATUS_OFFSET 1024
+
+/* ABI version qmoe_version() returns.  2: the dispatch meta array holds
+ * QMOE_META_INTS ints (was 4), and decode-block workspaces start with
+ * QMOE_DECODE_BLOCK_STATE_BYTES of call-to-call state (zeroed before first use). */
+#define QMOE_VERSION 2
 
 int qmoe_version(void);
 const char* qmoe_last_error(void);
@@ -159,28 +172,40 @@ int qmoe_moe_route_ws(const qmoe_bf16* x, const qmoe_bf16* w_router, const float
                       int32_t* tiles, int32_t* meta, void* workspace, int64_t workspace_bytes,
                       qmoe_stream_t stream);
 
-/* The whole MoE block at decode shape (T <= 8) in three launches: router
- * logits (with the post-attention RMSNorm fused when h is given); the expert
- * kernel (top-k in every workgroup, then work items of one touched expert and
- * 8 intermediate units each: gate/up rows, SwiGLU, and the matching down
- * block, accumulated into a per-workgroup partial output); and a fixed-order
- * reduction of the partials with the residual add:
+/* The whole MoE block at decode shape (T <= 8):
  *   xin = x, or bf16(rmsnorm(h) * rms_w) written to x_out
  *   out[t] = residual[t] + sum_j topk_w[t,j] * expert_{topk_idx[t,j]}(xin[t])
+ * At T = 1 with H = 2048, I = 768, k = 8, E <= 256 on a device with at least
+ * QMOE_DECODE_BLOCK_WGS compute units it is one launch (router, top-k,
+ * experts and combine; the workgroups exchange the router logits, the SwiGLU
+ * outputs and per-expert row sums through the workspace header).  Otherwise
+ * three launches: router logits (with the post-attention RMSNorm fused when
+ * h is given); the expert kernel (top-k in every workgroup, then work items
+ * of one touched expert and 8 intermediate units each: gate/up rows, SwiGLU,
+ * and the matching down block, accumulated into a per-workgroup partial
+ * output); and a fixed-order reduction of the partials with the residual.
  *   x: bf16 [T,H] or NULL; h: f32 [T,H] or NULL (exactly one of x, h);
  *   rms_w: bf16 [H] and x_out: bf16 [T,H] (with h); w_router: bf16 [E,H];
  *   bias: f32 [E] or NULL; w13: bf16 [E,2I,H] packed (QMOE_W13_GROUP);
  *   w2: bf16 [E, I/8, H, 8] blocked (QMOE_W2_BLOCK); residual: f32 [T,H] or
  *   NULL (may alias out and h); outputs logits f32 [T,E], topk_idx i32 [T,k],
- *   topk_w f32 [T,k]; workspace: device memory of at least
- *   qmoe_moe_decode_block_workspace(T, H) bytes (calls sharing it must not
- *   overlap); out: f32 [T,H].  Deterministic: every sum runs in a fixed order.
+ *   topk_w f32 [T,k]; out: f32 [T,H].
+ *   workspace: device memory of at least qmoe_moe_decode_block_workspace(T, H)
+ *   bytes, filled with zeros before its first use and otherwise left to the
+ *   library: its first QMOE_DECODE_BLOCK_STATE_BYTES carry call counters
+ *   from one call to the next (calls sharing a workspace, whatever their T,
+ *   must not overlap in time).  The 32-bit word at byte offset
+ *   QMOE_DECODE_BLOCK_STATUS_OFFSET becomes nonzero if a call's cross-
+ *   workgroup wait ever gave up (that call's outputs are NaN); it is never
+ *   set on a device where all QMOE_DECODE_BLOCK_WGS workgroups run at once.
+ *   Deterministic: every sum runs in a fixed order.
  *   Limits: T <= 8, T*k <= 64, E <= 256, k <= 16, H in {512, 1024, 2048,
  *   4096}, I % 32 == 0, I <= 1536.
  * Replaces: the decode MoE path of NeuronQwen3MoeDecoderLayer.forward
  *   (post_attention_layernorm -> router -> forward_selective_loading ->
  *   residual add, qwen_with_nki.py:10203-10207, 3456-3478) in the fusion order
- *   of _nki_fused_moe_block_decoder_forward (8518-8711). */
+ *   of _nki_fused_moe_block_decoder_forward and _nki_fused_moe_block_kernel
+ *   (8518-8711, 2184-2374: RMSNorm -> router -> experts -> residual). */
 int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* rms_w, float eps,
                           const qmoe_bf16* w_router, const float* bias, const qmoe_bf16* w13,
                           const qmoe_bf16* w2, const float* residual, int64_t T, int64_t H,
@@ -189,21 +214,23 @@ int qmoe_moe_decode_block(const qmoe_bf16* x, const float* h, const qmoe_bf16* r
                           qmoe_bf16* x_out, float* out, qmoe_stream_t stream);
 
 /* Workspace bytes qmoe_moe_decode_block needs for T tokens of width H
- * (QMOE_DECODE_BLOCK_WGS * T * H floats); -1 for negative sizes.
+ * (QMOE_DECODE_BLOCK_STATE_BYTES + QMOE_DECODE_BLOCK_WGS * T * H floats); -1
+ * for negative sizes.
  * Replaces: nothing in the reference (its kernels allocate their own HBM
  *   scratch, e.g. qwen_with_nki.py:1858); the caller owns memory here. */
 int64_t qmoe_moe_decode_block_workspace(int64_t T, int64_t H);
 
-/* qmoe_moe_decode_block without the workspace argument: the partial outputs
- * go to a static device array inside the library (16 MiB, one copy per GPU,
- * held until the process ends), so this call allocates nothing, not even on
- * its first use on a device.  Same arguments, kernels, limits and results as
+/* qmoe_moe_decode_block without the workspace argument: its workspace (the
+ * call-to-call state and the partial outputs) is a static device array
+ * inside the library (16.25 MiB, zero when the library loads, one copy per
+ * GPU, held until the process ends), so this call allocates nothing, not
+ * even on its first use on a device.  Same arguments, kernels, limits and results as
  * qmoe_moe_decode_block, plus T * H <= QMOE_DECODE_BLOCK_NOALLOC_MAX_TH (T <= 8
  * at H = 2048); larger sizes are rejected with QMOE_ERR_INVALID.  The device is
  * the current device, which must be the stream's.  Every call on one GPU shares
  * that GPU's array: calls that overlap in time on one GPU (other streams,
  * other host threads) race and must be ordered by the caller.  Nothing needs
- * clearing between calls (each call overwrites all the partials it reads).
+ * clearing between calls.
  * Replaces: nothing in the reference (no counterpart); it is for callers that
  *   cannot allocate device memory (code under HIP graph capture, tight
  *   serving loops, harnesses that forbid hipMalloc). */

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import json
 import os
 import shutil
 import subprocess
@@ -25,6 +26,7 @@ OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "qmoe", "libqmoe.so")
 PROBES = os.path.join(PKG, "probes")
 PROBE_LIB = os.path.join(PKG, "qmoe", "libqmoe_probe.so")
+BUILD_INFO = os.path.join(PKG, "qmoe", "build_info.json")
 ARCH = "gfx950"
 
 COMMON = [
@@ -81,7 +83,23 @@ def build(jobs: int = 8) -> str:
     if r.returncode != 0:
         raise RuntimeError("probe link failed:\n" + r.stdout + r.stderr)
     os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
+    _write_build_info()
     return LIB
+
+
+def _write_build_info() -> None:
+    """Record the commit the library was built from next to it (the GPU box
+    runs a copy of the tree without .git, so bench.py reads this file)."""
+    def git(*args):
+        try:
+            return subprocess.run(["git", *args], cwd=ROOT, capture_output=True, text=True,
+                                  timeout=10).stdout.strip()
+        except (OSError, subprocess.SubprocessError):
+            return ""
+    info = {"git": git("rev-parse", "--short", "HEAD") or None,
+            "dirty": bool(git("status", "--porcelain", "--untracked-files=no"))}
+    with open(BUILD_INFO, "w") as f:
+        json.dump(info, f)
 
 
 if __name__ == "__main__":

@@ -18,6 +18,6 @@ int fail(int code, const char* fmt, ...) {
 
 }  // namespace qmoe
 
-extern "C" int qmoe_version(void) { return 1; }
+extern "C" int qmoe_version(void) { return QMOE_VERSION; }
 
 extern "C" const char* qmoe_last_error(void) { return qmoe::g_last_error; }

@@ -119,6 +119,20 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// Workgroup barrier for LDS traffic: waits for the wave's own LDS (and
+// scalar) operations only.  __syncthreads() also waits for every global load
+// and store the wave has outstanding (its fence), which puts a memory round
+// trip on the critical path wherever a write-through store precedes it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The XCD (accelerator complex die, one of 8, each with its own L2) the
+// calling wave runs on.
+__device__ __forceinline__ int xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return int(v & 7);
+}
+
 // Non-temporal 16-byte load for weights that are streamed once.
 __device__ __forceinline__ u32x4 ld_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

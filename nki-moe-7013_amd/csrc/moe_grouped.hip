@@ -73,12 +73,6 @@ struct TileJob {
 constexpr int META_CTR = 4, META_DONE = 20;
 static_assert(META_DONE + 2 <= QMOE_META_INTS, "work counters fit in meta");
 
-__device__ __forceinline__ int xcc_id() {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return int(v & 7);
-}
-
 // The items of one launch in 8 shares: share v = [base(v), base(v) + n(v)).
 struct Queue {
   int32_t* ctr;  // meta[META_CTR + 8 * kind], one counter per share

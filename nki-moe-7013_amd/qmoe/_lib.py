@@ -22,9 +22,12 @@ GEMM_ADD_F32 = 2
 W13_GROUP = 32
 W2_BLOCK = 8
 GROUPED_MAX_TILE_M = 256
+VERSION = 2
 META_INTS = 24
 DECODE_BLOCK_WGS = 256
 DECODE_BLOCK_NOALLOC_MAX_TH = 16384
+DECODE_BLOCK_STATE_BYTES = 262144
+DECODE_BLOCK_STATUS_OFFSET = 1024
 
 P = c_void_p
 I64 = c_int64

@@ -438,12 +438,24 @@ def convert_qwen3_moe_hf_to_neuron_state_dict(state_dict, config: Qwen3MoeInfere
 
     layers = []
     E = config.num_experts
+    # Intermediate padding (qwen_with_nki.py:8959-8964, 8975-8985): zero units
+    # appended to every expert.  A zero gate/up row gives a zero SwiGLU
+    # output and a zero down column adds nothing, so the block output is the
+    # unpadded one; the padded width must still suit the kernels.
+    pad = int(getattr(config, "moe_intermediate_pad_size", 0) or 0)
+    if pad < 0:
+        raise ValueError(f"moe_intermediate_pad_size must be >= 0 (got {pad})")
+    if pad and (config.moe_intermediate_size + pad) % _lib.W13_GROUP:
+        raise ValueError(f"moe_intermediate_size + moe_intermediate_pad_size = "
+                         f"{config.moe_intermediate_size + pad} is not a multiple of {_lib.W13_GROUP}")
+    pad_rows = (lambda t: torch.nn.functional.pad(t, (0, 0, 0, pad))) if pad else (lambda t: t)
+    pad_cols = (lambda t: torch.nn.functional.pad(t, (0, pad))) if pad else (lambda t: t)
     for l in range(config.num_hidden_layers):
         p = f"layers.{l}."
         w13, w2 = weights.from_hf_experts(
-            [get(f"{p}mlp.experts.{e}.gate_proj.weight").float() for e in range(E)],
-            [get(f"{p}mlp.experts.{e}.up_proj.weight").float() for e in range(E)],
-            [get(f"{p}mlp.experts.{e}.down_proj.weight").float() for e in range(E)],
+            [pad_rows(get(f"{p}mlp.experts.{e}.gate_proj.weight").float()) for e in range(E)],
+            [pad_rows(get(f"{p}mlp.experts.{e}.up_proj.weight").float()) for e in range(E)],
+            [pad_cols(get(f"{p}mlp.experts.{e}.down_proj.weight").float()) for e in range(E)],
         )
         layers.append({
             "input_layernorm": put(get(f"{p}input_layernorm.weight")),

@@ -167,6 +167,15 @@ class Route:
             self.router_ws = torch.empty(need // 4, dtype=F32, device=device)
 
 
+def _need_meta(meta: torch.Tensor) -> None:
+    """The dispatch ``meta`` array must hold QMOE_META_INTS i32 (the library
+    writes and counts in all of them: a shorter array would be overrun)."""
+    if not isinstance(meta, torch.Tensor) or meta.dtype != I32 or not meta.is_contiguous():
+        raise ValueError("route.meta: expected a contiguous int32 tensor")
+    if meta.numel() < _lib.META_INTS:
+        raise ValueError(f"route.meta: needs {_lib.META_INTS} int32 (got {meta.numel()})")
+
+
 def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Optional[Route] = None) -> Route:
     T, k = topk_idx.shape
     _need(topk_idx, "topk_idx", I32)
@@ -174,6 +183,7 @@ def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Option
         route = Route.alloc(T, k, E, tile_m, topk_idx.device)
     if (route.T, route.k, route.E, route.tile_m) != (T, k, E, tile_m):
         raise ValueError("route buffers were allocated for a different shape")
+    _need_meta(route.meta)
     check(
         lib().qmoe_moe_permute(
             _ptr(topk_idx), T, k, E, tile_m, route.tiles.shape[0], _ptr(route.counts), _ptr(route.offsets),
@@ -198,6 +208,7 @@ def moe_route(x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[to
         route = Route.alloc(T, k, E, tile_m, x.device, with_topk=True)
     if (route.T, route.k, route.E, route.tile_m) != (T, k, E, tile_m) or route.topk_idx is None:
         raise ValueError("route buffers were allocated for a different shape / without top-k buffers")
+    _need_meta(route.meta)
     _same_device(x, w_router, bias, route.meta)
     route.ensure_router_ws(H, x.device)
     check(
@@ -239,6 +250,7 @@ def moe_experts_gemv(
     T, H, I, E = _check_experts(x, w13, w2)
     if (route.T, route.E) != (T, E):
         raise ValueError("route does not match x / w13")
+    _need_meta(route.meta)
     k = route.k
     dev = x.device
     act = torch.empty(T * k, I, dtype=F32, device=dev) if act is None else act
@@ -272,7 +284,7 @@ class DecodeBlockBuffers:
         return DecodeBlockBuffers(
             torch.empty(T, E, dtype=F32, device=device), torch.empty(T, k, dtype=I32, device=device),
             torch.empty(T, k, dtype=F32, device=device),
-            torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device),
+            torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device),
             torch.empty(T, H, dtype=BF16, device=device))
 
 
@@ -286,10 +298,13 @@ def moe_decode_block(
     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
     bufs: Optional[DecodeBlockBuffers] = None,
 ) -> torch.Tensor:
-    """Whole decode MoE block (T <= 8) in three launches (router logits;
-    top-k + fused gate/up/down work items with per-workgroup partial outputs;
-    fixed-order reduction + residual):
-    ``out = residual + MoE(x)`` with ``x`` given, or ``x = rmsnorm(h) * rms_w``."""
+    """Whole decode MoE block (T <= 8): one launch at T = 1 and the
+    Qwen3-30B-A3B shape, else three (router logits; top-k + fused
+    gate/up/down work items with per-workgroup partial outputs; fixed-order
+    reduction + residual):
+    ``out = residual + MoE(x)`` with ``x`` given, or ``x = rmsnorm(h) * rms_w``.
+    ``bufs.workspace`` carries state between calls (allocate it once, with
+    :meth:`DecodeBlockBuffers.alloc`, which zeroes it)."""
     if (x is None) == (h is None):
         raise ValueError("pass exactly one of x (bf16) and h (f32)")
     src = x if x is not None else h
@@ -341,6 +356,7 @@ def moe_experts_grouped(
     T, H, I, E = _check_experts(x, w13, w2)
     if (route.T, route.E) != (T, E) or not 0 < route.tile_m <= _lib.GROUPED_MAX_TILE_M:
         raise ValueError(f"route must match x / w13 and use tile_m <= {_lib.GROUPED_MAX_TILE_M}")
+    _need_meta(route.meta)
     k = route.k
     dev = x.device
     act = torch.empty(T * k, I, dtype=BF16, device=dev) if act is None else act

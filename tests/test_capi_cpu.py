@@ -45,7 +45,21 @@ def test_header_constants_match_python_mirror():
 
 
 def test_version():
-    assert _lib.lib().qmoe_version() == 1
+    assert _lib.lib().qmoe_version() == _lib.VERSION == 2
+
+
+def test_route_meta_length_checked():
+    """A dispatch meta shorter than QMOE_META_INTS is refused before any
+    launch (the library writes and counts in all of its ints)."""
+    import torch
+
+    from qmoe import ops
+
+    ops._need_meta(torch.zeros(_lib.META_INTS, dtype=torch.int32))
+    with pytest.raises(ValueError, match="needs 24"):
+        ops._need_meta(torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="int32"):
+        ops._need_meta(torch.zeros(_lib.META_INTS, dtype=torch.int64))
 
 
 @pytest.mark.parametrize(
@@ -139,8 +153,10 @@ def test_check_maps_status_to_exceptions():
 
 def test_decode_block_workspace_size():
     lib = _lib.lib()
-    assert lib.qmoe_moe_decode_block_workspace(1, 2048) == _lib.DECODE_BLOCK_WGS * 2048 * 4
-    assert lib.qmoe_moe_decode_block_workspace(8, 512) == _lib.DECODE_BLOCK_WGS * 8 * 512 * 4
+    st = _lib.DECODE_BLOCK_STATE_BYTES
+    assert lib.qmoe_moe_decode_block_workspace(1, 2048) == st + _lib.DECODE_BLOCK_WGS * 2048 * 4
+    assert lib.qmoe_moe_decode_block_workspace(8, 512) == st + _lib.DECODE_BLOCK_WGS * 8 * 512 * 4
+    assert lib.qmoe_moe_decode_block_workspace(0, 2048) == st
     assert lib.qmoe_moe_decode_block_workspace(-1, 2048) == -1
 
 

@@ -917,6 +917,109 @@ def test_moe_decode_block(dev, experts, router_w, T, normed):
     assert_close_layer(outs[0].cpu()[rows] - residual.cpu()[rows], ref, f"decode block T={T}", 2e-3, 1e-4)
 
 
+def _decode_status(bufs) -> int:
+    """Status word of a decode-block workspace (nonzero once a wait gave up)."""
+    off = _lib.DECODE_BLOCK_STATUS_OFFSET
+    return int(bufs.workspace[off:off + 4].view(torch.int32).item())
+
+
+def test_moe_decode_block_fused_state(dev, experts, router_w):
+    """The single-launch T = 1 block carries call counters and tagged exchange
+    slots in its workspace: 40 calls on one workspace with inputs changing
+    from call to call each equal the same call on a fresh workspace (bitwise);
+    three-launch T = 8 calls interleaved on the same workspace (their partials
+    sit after the state) leave it intact; the status word stays 0."""
+    announce("fused decode block: workspace state over 40 calls")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(77)
+    bufs8 = ops.DecodeBlockBuffers.alloc(8, H, I, E, K_TOP, dev)
+    bufs1 = ops.DecodeBlockBuffers(bufs8.logits[:1], bufs8.topk_idx[:1], bufs8.topk_w[:1], bufs8.workspace,
+                                   bufs8.x_out[:1])
+    xs = [bf16_randn((1, H), g, dev) for _ in range(5)]
+    res = torch.randn(1, H, generator=g, device=dev)
+    fresh = lambda T: ops.DecodeBlockBuffers.alloc(T, H, I, E, K_TOP, dev)
+    refs = [ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x, residual=res, bufs=fresh(1)) for x in xs]
+    x8 = bf16_randn((8, H), g, dev)
+    res8 = torch.randn(8, H, generator=g, device=dev)
+    ref8 = ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x8, residual=res8, bufs=fresh(8))
+    for i in range(40):
+        got = ops.moe_decode_block(router_w, w13, w2, K_TOP, x=xs[i % 5], residual=res, bufs=bufs1)
+        assert torch.equal(got, refs[i % 5]), f"call {i}"
+        if i % 7 == 3:
+            assert torch.equal(ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x8, residual=res8, bufs=bufs8),
+                               ref8), f"T=8 call after {i}"
+    torch.cuda.synchronize()
+    assert _decode_status(bufs8) == 0
+
+
+def test_moe_decode_block_fused_graph_replays(dev, experts, router_w):
+    """The single-launch block captured in a HIP graph: every replay (with
+    eager calls on the same workspace between replays) equals eager."""
+    announce("fused decode block: graph replays")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(78)
+    bufs = ops.DecodeBlockBuffers.alloc(1, H, I, E, K_TOP, dev)
+    x = bf16_randn((1, H), g, dev)
+    x_other = bf16_randn((1, H), g, dev)
+    res = torch.randn(1, H, generator=g, device=dev)
+    out = torch.empty(1, H, device=dev)
+    ref = ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x, residual=res,
+                               bufs=ops.DecodeBlockBuffers.alloc(1, H, I, E, K_TOP, dev))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x, residual=res, out=out, bufs=bufs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x, residual=res, out=out, bufs=bufs)
+    for rep in range(6):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {rep}"
+        ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x_other, residual=res, bufs=bufs)
+        torch.cuda.synchronize()
+    assert _decode_status(bufs) == 0
+
+
+@pytest.mark.parametrize("n_exp", [64, 256])
+def test_moe_decode_block_fused_expert_counts(dev, n_exp):
+    """The single-launch block at E = 64 (one key register per lane) and
+    E = 256 (four), normed and not: routing exact where the gap allows, the
+    output vs the oracle on the token's experts."""
+    w_r = bf16_randn((n_exp, H), torch.Generator(device=dev).manual_seed(5 + n_exp), dev, std=0.02)
+    g = torch.Generator(device=dev).manual_seed(600 + n_exp)
+    w13 = bf16_randn((n_exp, 2 * I, H), g, dev, std=0.02)
+    w2 = bf16_randn((n_exp, I // 8, H, 8), g, dev, std=0.02)
+    rms_w = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    for normed in (False, True):
+        announce(f"fused decode block E={n_exp} normed={normed}")
+        h = torch.randn(1, H, generator=g, device=dev)
+        res = torch.randn(1, H, generator=g, device=dev)
+        bufs = ops.DecodeBlockBuffers.alloc(1, H, I, n_exp, K_TOP, dev)
+        if normed:
+            out = ops.moe_decode_block(w_r, w13, w2, K_TOP, h=h, rms_w=rms_w, eps=1e-6, residual=res, bufs=bufs)
+        else:
+            out = ops.moe_decode_block(w_r, w13, w2, K_TOP, x=h.to(torch.bfloat16), residual=res, bufs=bufs)
+        torch.cuda.synchronize()
+        xin = bufs.x_out.cpu() if normed else h.to(torch.bfloat16).cpu()
+        rl, rw, ri = oracle.router_topk(xin, w_r.cpu(), K_TOP)
+        assert max_abs(bufs.logits, rl) <= 1e-4
+        idx = bufs.topk_idx.cpu().long()
+        if bool(gap_mask(rl, K_TOP)[0]):
+            assert torch.equal(idx, ri)
+            np.testing.assert_allclose(bufs.topk_w.cpu().numpy(), rw.numpy(), rtol=2e-5, atol=1e-7)
+        else:  # near-tied k-th logit: the oracle takes the product's experts, weights from its own logits
+            sel = rl.gather(1, idx)
+            rw = torch.softmax(sel, dim=1)
+            ri = idx
+        ref = _oracle_rows(xin, ri, rw, _ExpertCache(w13, w2), [0])
+        assert_close_layer(out.cpu() - res.cpu(), ref, f"fused block E={n_exp}", 2e-3, 1e-4)
+        assert _decode_status(bufs) == 0
+
+
 # --------------------------------------------------------------------------- embedding / greedy argmax
 def test_embed_gather_and_bad_ids(dev):
     announce("embedding gather")

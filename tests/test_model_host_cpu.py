@@ -84,6 +84,31 @@ def test_converter_key_mapping_and_layouts(prefix):
             assert torch.equal(down[e], bf(sd[ex + "down_proj.weight"]).t())
 
 
+def test_converter_pads_intermediate_with_zero_units():
+    """moe_intermediate_pad_size (qwen_with_nki.py:8959-8964): zero units are
+    appended to every expert's gate, up and down; each expert's SwiGLU output
+    is unchanged, and a padded width the kernels cannot take is refused."""
+    import oracle
+
+    sd = _hf_state_dict(seed=3)
+    ref = qm.convert_qwen3_moe_hf_to_neuron_state_dict(sd, _config())
+    out = qm.convert_qwen3_moe_hf_to_neuron_state_dict(sd, _config(moe_intermediate_pad_size=32))
+    x = torch.randn(3, H, generator=torch.Generator().manual_seed(9))
+    for l in range(L):
+        gu, dn = weights.unpack_gate_up(out["layers"][l]["w13"]), weights.unpack_down(out["layers"][l]["w2"])
+        gu0, dn0 = weights.unpack_gate_up(ref["layers"][l]["w13"]), weights.unpack_down(ref["layers"][l]["w2"])
+        assert gu.shape == (E, H, 2 * (I + 32)) and dn.shape == (E, I + 32, H)
+        assert torch.equal(gu[:, :, :I], gu0[:, :, :I]) and torch.equal(gu[:, :, I + 32: 2 * I + 32], gu0[:, :, I:])
+        assert not gu[:, :, I: I + 32].any() and not gu[:, :, 2 * I + 32:].any()
+        assert torch.equal(dn[:, :I], dn0) and not dn[:, I:].any()
+        for e in range(E):
+            a = oracle.expert_swiglu(x, gu[e].float(), dn[e].float())
+            b = oracle.expert_swiglu(x, gu0[e].float(), dn0[e].float())
+            assert torch.allclose(a, b, rtol=1e-6, atol=1e-6)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        qm.convert_qwen3_moe_hf_to_neuron_state_dict(sd, _config(moe_intermediate_pad_size=16))
+
+
 def test_converter_lm_head_tied_and_missing():
     sd = _hf_state_dict(lm_head=False)
     out = qm.convert_qwen3_moe_hf_to_neuron_state_dict(sd, _config(tie_word_embeddings=True))

@@ -1,9 +1,11 @@
 """The allocation-free decode MoE block (qmoe_moe_decode_block_noalloc).
 
 Called through the C ABI with ctypes and checked against the workspace entry
-point qmoe_moe_decode_block on the same inputs: two calls in a row on one GPU,
-the second with fewer tokens than the first, so the second reads a static
-scratch array that still holds the first call's partials.  Both entry points
+point qmoe_moe_decode_block on the same inputs: calls in a row on one GPU,
+each later one with fewer tokens than the first, so they read a static
+scratch array that still holds the first call's partials.  At I = 768 the
+T = 1 calls take the single-launch path, whose call counters and exchange
+slots live in the same static array (two T = 1 calls in a row).  Both entry points
 run the same kernels in the same fixed summation order, so the bar is
 bit-equality of the block output, the router logits, the top-k ids and the
 top-k weights.
@@ -20,7 +22,7 @@ from qmoe import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
-H, E, I, K_TOP = 2048, 128, 256, 8
+H, E, K_TOP = 2048, 128, 8
 
 
 def _ptr(t):
@@ -29,6 +31,7 @@ def _ptr(t):
 
 def _noalloc(w_router, w13, w2, x, h, rms_w, residual, T):
     dev = w13.device
+    I = w13.shape[1] // 2
     logits = torch.full((T, E), float("nan"), device=dev)
     idx = torch.full((T, K_TOP), -1, dtype=torch.int32, device=dev)
     w = torch.full((T, K_TOP), float("nan"), device=dev)
@@ -42,15 +45,16 @@ def _noalloc(w_router, w13, w2, x, h, rms_w, residual, T):
     return out, logits, idx, w, x_out
 
 
+@pytest.mark.parametrize("I, Ts", [(256, (8, 3)), (768, (8, 1, 1))])
 @pytest.mark.parametrize("normed", [False, True])
-def test_noalloc_decode_block_matches_workspace_entry(dev, normed):
-    g = torch.Generator(device=dev).manual_seed(4242 + int(normed))
+def test_noalloc_decode_block_matches_workspace_entry(dev, normed, I, Ts):
+    g = torch.Generator(device=dev).manual_seed(4242 + int(normed) + I)
     w_router = bf16_randn((E, H), g, dev, 0.02)
     w13 = bf16_randn((E, 2 * I, H), g, dev, 0.02)
     w2 = bf16_randn((E, I // 8, H, 8), g, dev, 0.02)
     rms_w = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
-    for T in (8, 3):  # the second call is smaller than the first
-        announce(f"noalloc decode block T={T} normed={normed}")
+    for T in Ts:  # the later calls are smaller than the first
+        announce(f"noalloc decode block T={T} I={I} normed={normed}")
         h = torch.randn(T, H, generator=g, device=dev)
         residual = torch.randn(T, H, generator=g, device=dev)
         if normed:
