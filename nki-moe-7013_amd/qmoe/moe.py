@@ -125,6 +125,7 @@ class MoEBlock:
         self.experts = ExpertMLPs(w13, w2, top_k)
         self.top_k = top_k
         self.last_routing = None
+        self.last_input = None  # the bf16 rows the router last saw (for checks)
         self._bufs = {}
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
@@ -137,9 +138,11 @@ class MoEBlock:
             out = ops.moe_decode_block(self.w_router, ex.w13, ex.w2, self.top_k, x=x, bias=self.router_bias,
                                        residual=residual, out=out, bufs=bufs)
             self.last_routing = (bufs.logits, bufs.topk_w, bufs.topk_idx)
+            self.last_input = x
             return out
         route = ops.moe_route(x, self.w_router, self.top_k, self.router_bias, TILE_M)
         self.last_routing = (route.logits, route.topk_w, route.topk_idx)
+        self.last_input = x
         if T <= GEMV_MAX_TOKENS:
             y = ops.moe_experts_gemv(x, ex.w13, ex.w2, route)
         else:
@@ -157,6 +160,7 @@ class MoEBlock:
             out = ops.moe_decode_block(self.w_router, ex.w13, ex.w2, self.top_k, h=h, rms_w=rms_w, eps=eps,
                                        bias=self.router_bias, residual=residual, out=out, bufs=bufs)
             self.last_routing = (bufs.logits, bufs.topk_w, bufs.topk_idx)
+            self.last_input = bufs.x_out
             return out
         x = ops.rmsnorm_residual(h, rms_w, eps)
         return self.forward(x, residual, out)

@@ -98,3 +98,36 @@ def oracle_rows(x, top_i, top_w, cache, rows):
         acc = torch.stack([oracle.expert_swiglu(xs, *cache[int(e)])[0] for e in top_i[t]])
         out.append(torch.sum(acc * top_w[t].float().unsqueeze(1), dim=0))
     return torch.stack(out)
+
+
+def check_layer_moe(out, base, y_ref, moe, top_k, what):
+    """The MoE half of a decoder-layer step, held to the accuracy contract.
+
+    ``out`` [N, H]: the product's layer output rows; ``base`` [N, H]: the fp32
+    reference residual stream after attention; ``y_ref`` [N, H]: the fp32
+    reference post-attention normed rows; ``moe``: the layer's MoEBlock (its
+    last routing and the bf16 rows its router saw).
+    1. The oracle routes from the product's own bf16 normed rows: expert ids
+       exact wherever the k-th / (k+1)-th logit gap exceeds 1e-3.
+    2. On every such row, the layer output within max-abs 2e-2 / mean
+       relative 5e-3 of base + the oracle MoE of the fp32 normed row over
+       those experts (weights: softmax of the fp32 row's logits over them;
+       on rows where fp32 routing agrees this is the fp32 reference layer).
+    3. Secondary, against fp32 routing: agreement on every row with a 1e-2
+       gap and on at least 90% of rows."""
+    router = moe.w_router
+    idx = moe.last_routing[2].cpu().long()
+    xhat = moe.last_input.cpu()
+    rl, _, ri = oracle.router_topk(xhat, router.cpu(), top_k)
+    ok = gap_mask(rl, top_k)
+    assert torch.equal(idx[ok], ri[ok]), f"{what}: expert ids differ where the gap exceeds {GAP}"
+    rows = [t for t in range(idx.shape[0]) if bool(ok[t])]
+    assert rows, f"{what}: no row with a clear router gap"
+    yl = y_ref.float().cpu() @ router.float().cpu().t()
+    w = torch.softmax(yl.gather(1, ri), dim=1)
+    ref = base.float().cpu()[rows] + oracle_rows(y_ref.cpu(), ri, w, ExpertCache(moe.experts.w13, moe.experts.w2),
+                                                 rows)
+    assert_close_layer(out.float().cpu()[rows], ref, what)
+    same, gap = routing_agreement(y_ref.cpu(), router.cpu(), top_k, idx)
+    assert bool(same[gap > 1e-2].all()), f"{what}: routing differs on a row with a clear fp32 router gap"
+    assert same.float().mean() >= 0.9, f"{what}: fp32 routing agrees on {float(same.float().mean()):.2f} of rows"
