@@ -402,7 +402,8 @@ int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_cache, const 
  * qmoe_qkv_finish (q/k RMSNorm, RoPE, the new K/V row into the cache at
  * positions[b]) and qmoe_attn_decode_bucket in one split launch + the merge,
  * with the same result bits as those two calls.  Row b sees cache entries
- * [0, positions[b]] (at most max_ctx of them); a position outside [0,
+ * [0, positions[b]], at most the first max_ctx of them (a position at or
+ * past max_ctx still writes its K/V row); a position outside [0,
  * min(S_max, max_pos)) writes nothing and gets zeros.
  *   qkv: f32 [B, (Hq + 2*Hkv)*D] (qmoe_gemv_rmsnorm / qmoe_gemm with
  *   QMOE_GEMM_STORE_F32); q_norm_w, k_norm_w: bf16 [D]; rope_cos, rope_sin:

@@ -783,6 +783,9 @@ __global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
   // the K/V stream, so the finish waits for them alone
   constexpr int HPW = FUSED ? (AD_MAX_G + SUBS - 1) / SUBS : 1;  // q heads per wave, at most
   const bool owner = FUSED && pos < ctx && pos >= kw0 && pos < kw0 + AD_WKEYS;  // wave-uniform
+  // a position at or past max_ctx lies in no visible key range: split 0's
+  // wave 0 still stores its K/V row (as qmoe_qkv_finish would)
+  const bool writer = owner || (FUSED && pos >= ctx && blockIdx.x == 0 && wave == 0);
   // (the first 8 heads branch-free, heads past G loading head G - 1 again;
   // heads 8-15 behind one test; a scheduling barrier keeps all of it ahead
   // of the K/V requests, so the finish waits for these loads alone)
@@ -858,7 +861,7 @@ __global__ __launch_bounds__(SUBS * 64) void attn_decode_split_kernel(
         qs[h * HD + lane + 64] = f32_to_bf16(rhi[i]);
       }
     }
-    if (owner) {
+    if (writer) {
       finish_head(nlo[0], nhi[0], bf16_to_f32(wk[0]), bf16_to_f32(wk[1]), c, sn, fin.eps);
       const int64_t row = kv_base + int64_t(pos) * HD;
       const uint16_t k0 = f32_to_bf16(nlo[0]), k1 = f32_to_bf16(nhi[0]);

@@ -93,18 +93,16 @@ class Attention:
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
                 cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start=0,
-                ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None,
-                norm: Optional[tuple] = None) -> torch.Tensor:
+                max_ctx: Optional[int] = None, norm: Optional[tuple] = None) -> torch.Tensor:
         """``x[B*S, H]`` bf16 (input-normed), ``residual[B*S, H]`` f32 (updated
         in place), ``positions[B*S]`` i32 (RoPE position == cache index).
 
         S > 1: causal prefill of a chunk starting at cache index ``start`` (an
         int, or an int32 ``[1]`` device tensor for graph replays at any position).
-        S == 1: decode; ``ctx_len[B]`` i32 = visible cache entries (position + 1),
-        at most ``max_ctx`` when a context bucket is given.  On the GEMV path
-        (B <= 16 decode rows) the finish runs inside the attention launch
-        (``attn_decode_fused``), which sees entries ``[0, position]``: there
-        ``ctx_len`` must be ``positions + 1`` and is not read.
+        S == 1: decode; row b sees cache entries ``[0, positions[b]]`` (at most
+        the first ``max_ctx`` when a context bucket is given), on every path.
+        On the GEMV path (B <= 16 decode rows) the finish runs inside the
+        attention launch (``attn_decode_fused``).
         ``norm = (rms_w, eps)``: ``x`` is the fp32 residual row itself (B*S == 1)
         and the input RMSNorm is fused into the QKV GEMV.
         """
@@ -140,9 +138,7 @@ class Attention:
             elif S > 1:
                 o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
             else:
-                if ctx_len is None:
-                    ctx_len = positions + 1
-                o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, ctx_len, self.scale,
+                o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, positions + 1, self.scale,
                                     self._decode_ws(B, cache, x.device), max_ctx=max_ctx)
         key = ("oproj", o.shape[0])
         if key not in self._ws:  # split-K scratch for prefill-size token counts (None: not split)

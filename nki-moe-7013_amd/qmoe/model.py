@@ -164,17 +164,17 @@ class NeuronQwen3MoeDecoderLayer:
         self._rope = None  # (cos, sin) built from head_dim / rope_theta on first use
 
     def run(self, h: torch.Tensor, positions: torch.Tensor, B: int, S: int, rope, start=0,
-            ctx_len: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
+            max_ctx: Optional[int] = None) -> torch.Tensor:
         """In-place layer on the fp32 residual ``h[B*S, H]``."""
         eps = self.input_layernorm.eps
         if B * S == 1 and ops.qkv_norm_rope_workspace(1, h.shape[1], self.self_attn.n_q, self.self_attn.n_kv,
                                                       self.self_attn.head_dim) > 0:
             # one-token step: the input RMSNorm runs inside the QKV GEMV's staging
-            self.self_attn.forward(h, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx,
+            self.self_attn.forward(h, h, positions, B, S, self.cache, rope[0], rope[1], start, max_ctx,
                                    norm=(self.input_layernorm.weight, eps))
         else:
             x = ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
-            self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, ctx_len, max_ctx)
+            self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, max_ctx)
         self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
         return h
 
@@ -252,7 +252,7 @@ class NeuronQwen3MoeDecoderLayer:
         if S > 1:
             self.run(h, pos, B, S, rope, int(starts[0]))
         else:
-            self.run(h, pos, B, 1, rope, 0, ctx_len=(pos + 1).contiguous())
+            self.run(h, pos, B, 1, rope, 0)
         out = h.view(B, S, H).to(hidden_states.dtype)
         return out, self.cache, rope[0], rope[1], None
 
@@ -300,12 +300,11 @@ class NeuronQwen3MoeModel:
             l.cache = KVCache(B, c.num_key_value_heads, S_max, c.head_dim, self.embed_tokens.device)
 
     def hidden(self, input_ids: torch.Tensor, positions: torch.Tensor, B: int, S: int, start,
-               ctx_len: Optional[torch.Tensor] = None, h_buf: Optional[torch.Tensor] = None,
-               max_ctx: Optional[int] = None) -> torch.Tensor:
+               h_buf: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
         """fp32 final hidden states ``[B*S, H]`` (before the final norm)."""
         h = ops.embed(input_ids.reshape(-1).long(), self.embed_tokens, out=h_buf, err=self.embed_err)
         for layer in self.layers:
-            layer.run(h, positions, B, S, self.rope, start, ctx_len, max_ctx)
+            layer.run(h, positions, B, S, self.rope, start, max_ctx)
         return h
 
     def check_embed(self) -> None:
@@ -580,7 +579,7 @@ class NeuronQwen3MoeForCausalLM:
         else:
             pos = positions.to(device=dev, dtype=torch.int32).contiguous()
             self.position = int(pos.max()) + 1
-        h = self.model.hidden(token_ids.to(dev).view(B, 1), pos, B, 1, 0, ctx_len=pos + 1)
+        h = self.model.hidden(token_ids.to(dev).view(B, 1), pos, B, 1, 0)
         return self.model.logits(h)
 
     def forward(self, input_ids: torch.Tensor, attention_mask=None, position_ids=None, **kw) -> CausalLMOutput:
@@ -658,8 +657,7 @@ class NeuronQwen3MoeForCausalLM:
         # no reduction that records a memset into the graph (torch's argmax
         # over a 151,936-wide row would), so replays stay correct.
         def step():
-            ctx = st["pos"] + 1
-            h = m.hidden(st["tok"].view(B, 1), st["pos"], B, 1, 0, ctx_len=ctx, h_buf=st["h"], max_ctx=bucket)
+            h = m.hidden(st["tok"].view(B, 1), st["pos"], B, 1, 0, h_buf=st["h"], max_ctx=bucket)
             m.logits(h, out=st["logits"])
             ops.argmax(st["logits"], out=st["tok"], workspace=st["am_ws"])
             st["pos"].add_(1)

@@ -628,7 +628,7 @@ def test_attention_layer_B8_prefill1024_decode_to_8192(dev, attn_w):
         pd = torch.full((B,), p, device=dev, dtype=torch.int32)
         out = torch.zeros(B, H, device=dev)
         past = (cache.k[:, :, :p].float().clone(), cache.v[:, :, :p].float().clone())
-        att.forward(xd, out, pd, B, 1, cache, cos, sin, 0, ctx_len=pd + 1, max_ctx=max_ctx)
+        att.forward(xd, out, pd, B, 1, cache, cos, sin, 0, max_ctx=max_ctx)
         torch.cuda.synchronize()
         r, _ = oracle.attention_layer(xd.float().view(B, 1, H), w, pd.view(B, 1).long(), c, past)
         assert_close_layer(out.cpu(), r.reshape(B, H).cpu(), f"attention decode {label}")
@@ -686,12 +686,14 @@ def test_qkv_finish_matches_qkv_norm_rope(dev, attn_w):
 
 
 # (B, Hq, Hkv, S_max, positions, bucket): the new key first in the cache, last
-# and first of a 64-key wave, G = 16 and G = 1, and 8 rows at a capacity of
-# 8193 (four waves per split workgroup, keys up to the last cache row).
+# and first of a 64-key wave, G = 16 and G = 1, 8 rows at a capacity of 8193
+# (four waves per split workgroup, keys up to the last cache row), and
+# positions at or past the bucket (the row is written, not attended to).
 @pytest.mark.parametrize("B,Hq_,Hkv_,S_max,pos,bucket", [
     (1, 32, 4, 2048, [0], None), (1, 32, 4, 2048, [63], 1024), (1, 32, 4, 2048, [64], 1024),
     (3, 32, 4, 2048, [700, 5, 1023], 1024), (2, 32, 2, 512, [100, 511], None), (2, 4, 4, 512, [10, 300], None),
-    (8, 32, 4, 8193, [1279, 0, 255, 256, 4000, 8192, 63, 64], None)])
+    (8, 32, 4, 8193, [1279, 0, 255, 256, 4000, 8192, 63, 64], None),
+    (3, 32, 4, 2048, [1024, 100, 2047], 1024), (1, 32, 4, 2048, [1500], 256)])
 def test_attn_decode_fused_matches_finish_then_decode(dev, B, Hq_, Hkv_, S_max, pos, bucket):
     """qmoe_attn_decode_fused gives the bits of qmoe_qkv_finish followed by the
     decode attention over ctx = position + 1: the same output and the same

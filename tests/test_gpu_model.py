@@ -54,8 +54,7 @@ def test_decoder_layer_prefill_then_decode(dev, B, S, steps):
         x = torch.randn(B, n, cfg.hidden_size, generator=g, device=dev)
         pos = (p0 + torch.arange(n, device=dev)).expand(B, n)
         h = x.reshape(B * n, -1).contiguous().clone()
-        layer.run(h, pos.reshape(-1).to(torch.int32).contiguous(), B, n, rope, p0,
-                  (pos[:, -1] + 1).to(torch.int32).contiguous() if n == 1 else None)
+        layer.run(h, pos.reshape(-1).to(torch.int32).contiguous(), B, n, rope, p0)
         ref, past = oracle.decoder_layer(x, w, pos, c, past)
         a, _ = oracle.attention_layer(oracle.rmsnorm(x, w["input_layernorm"], c["eps"]), w, pos, c,
                                       None if step == 0 else (past[0][:, :, :-1], past[1][:, :, :-1]))
