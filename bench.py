@@ -587,13 +587,12 @@ def bench_attention(dev, B=8, S=1024, ctx_points=(1280, 8192), reps=10):
     rd = torch.zeros(B, Hd, device=dev)
     for L in ctx_points:
         pd = torch.full((B,), L - 1, device=dev, dtype=torch.int32)
-        cl = pd + 1
 
         byts = ((Hq + 2 * Hkv) * D * Hd + Hd * Hq * D) * 2 + B * Hkv * L * D * 2 * 2
         bucket = min(cap, 1 << max(8, (L - 1).bit_length()))  # the model's decode-graph bucket
         for tag, mc in (("", bucket), ("_full_launch", None)):
             def dec():
-                att.forward(xd, rd, pd, B, 1, cache, cos, sin, 0, cl, max_ctx=mc)
+                att.forward(xd, rd, pd, B, 1, cache, cos, sin, 0, max_ctx=mc)
 
             secs, ev_secs, done = time_graph(dec, 1, 200, 20)
             us = ev_secs / done * 1e6

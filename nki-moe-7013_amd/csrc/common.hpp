@@ -15,6 +15,10 @@ namespace qmoe {
 // returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Compute units of the current device (queried once per device; 0 when the
+// query fails).
+int current_device_cus();
+
 inline int hip_status(const char* where) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(QMOE_ERR_HIP, "%s: %s", where, hipGetErrorString(e));

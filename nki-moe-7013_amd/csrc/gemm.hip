@@ -244,6 +244,93 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const uint16_t* __restri
   }
 }
 
+// Skinny GEMM for 2 <= M <= 8 rows of A (batched decode) with the weights
+// streamed through LDS: K = 512 * WAVES, wave w owns k in [512 w, 512 w +
+// 512), a workgroup owns NB output columns (one workgroup per CU at the
+// decode shapes: 20 for N = 5120, 8 for N = 2048).  Each wave copies its NB
+// weight rows (1 KB each) into LDS with one non-temporal LDS-DMA per row (64
+// lanes x 16 contiguous bytes: whole 128-byte lines, the access the one-row
+// GEMV streams at), rows GV_ROWB = 1040 bytes apart so the 16 rows of an MFMA
+// B fragment fall on distinct LDS banks.
+// The A fragments come straight from global memory (the activation rows are
+// L2-resident) and are loaded packed: the 16x16x32 MFMA has 16 A rows and
+// only rows 0-7 are live, so lane (c, g) loads 8 k-values of row c % 8 at
+// step 2p + c / 8 and a DPP rotation by 8 within each row of 16 lanes hands
+// step 2p + 1 to lanes 0-7 (rows 8-15 of the product are never read).  Every
+// lane's load is live: half the A load instructions of a zero-padded
+// fragment, which is what an 8-row GEMV pays for (the A bytes per workgroup
+// equal the weight bytes at 8 columns).  The waves' 8 x NB partials are added
+// in k order through LDS.
+constexpr int GV_ROWB = 1040;
+template <int WAVES, int NB, int MODE>
+__global__ __launch_bounds__(64 * WAVES) void gemv_pk_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                             const uint16_t* __restrict__ B, int M, int N,
+                                                             int K, void* __restrict__ C, int64_t ldc) {
+  constexpr int NT = (NB + 15) / 16;  // 16-column MFMA tiles
+  __shared__ __attribute__((aligned(1024))) uint8_t wl[WAVES][NB * GV_ROWB];
+  __shared__ float red[WAVES][8][NB + 1];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int n0 = blockIdx.x * NB;
+  const int kw = wave * 512;
+  const int col = lane & 15, kg = lane >> 4;
+  u32x4 ap[8];  // ap[p]: row col % 8, k = kw + (2p + col / 8) * 32 + 8 kg .. + 8
+  {
+    const uint16_t* p = A + min(col & 7, M - 1) * lda + kw + (col >> 3) * 32 + kg * 8;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ap[s] = ld16(p + s * 64);
+  }
+  {
+    const pipe::i32x4 rb = pipe::make_rsrc(B, uint32_t(int64_t(N) * K * 2));
+    const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>(&wl[wave][0]));
+#pragma unroll
+    for (int r = 0; r < NB; ++r) {
+      const uint32_t off = n0 + r < N ? uint32_t((int64_t(n0 + r) * K + kw) * 2) + lane * 16u : pipe::PAD;
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                   :
+                   : "s"(lds0 + uint32_t(r * GV_ROWB)), "v"(off), "s"(rb)
+                   : "memory");
+    }
+  }
+  pipe::wait_vm<0>();  // this wave's weight rows are in LDS (and its A fragments in registers)
+  f32x4 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = f32x4{};
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    u32x4 a = ap[s >> 1];
+    if (s & 1) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) a[d] = __builtin_amdgcn_update_dpp(0u, a[d], 0x128, 0xf, 0xf, false);  // row_ror:8
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const u32x4 b = *reinterpret_cast<const u32x4*>(&wl[wave][0] + min(j * 16 + col, NB - 1) * GV_ROWB +
+                                                      kg * 16 + s * 64);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc[j], 0, 0, 0);
+    }
+  }
+  // lane l holds column l % 16 of tile j, rows (l / 16) * 4 + 0..3; rows 8-15 are not used
+  if (kg < 2) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      if (j * 16 + col < NB)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][kg * 4 + i][j * 16 + col] = acc[j][i];
+  }
+  __syncthreads();
+  for (int i = t; i < 8 * NB; i += 64 * WAVES) {
+    const int m = i / NB, n = i % NB;
+    if (m < M && n0 + n < N) {
+      float v = red[0][m][n];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) v += red[w][m][n];
+      store_out<MODE>(C, int64_t(m) * ldc + n0 + n, v);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ MFMA tile
 // Grid = every (row tile, column tile) pair, renumbered XCD-contiguously and
 // then walked in groups of 8 row tiles per column sweep, so the workgroups
@@ -651,10 +738,40 @@ static int launch_gemv_mfma(const uint16_t* A, int64_t lda, const uint16_t* B, i
 }
 
 template <int MODE>
+static int launch_gemv_pk(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
+                          void* C, int64_t ldc, hipStream_t s) {
+  // the most columns per workgroup that still leaves one workgroup per CU
+  // (fewer workgroups load the A rows fewer times: at 8 rows the QKV shape N
+  // = 5120, K = 2048 runs 7.3 / 6.5 / 6.0 us at 8 / 10 / 20 columns, and
+  // o_proj N = 2048, K = 4096 5.7 us at 8 columns against 7.2 at 4)
+  const int cus = current_device_cus();
+  const int nb = N >= 20 * cus && K <= 2048 ? 20 : N >= 16 * cus ? 16 : N >= 8 * cus ? 8 : 4;
+#define QMOE_PK(W, NB_)                                                                            \
+  if (K == 512 * W && nb == NB_) {                                                                 \
+    hipLaunchKernelGGL((gemv_pk_kernel<W, NB_, MODE>), dim3(unsigned((N + NB_ - 1) / NB_)), dim3(64 * W), 0, \
+                       s, A, lda, B, M, N, K, C, ldc);                                             \
+    return hip_status("qmoe_gemm(gemv pk)");                                                       \
+  }
+#define QMOE_PK_W(W) QMOE_PK(W, 4) QMOE_PK(W, 8) QMOE_PK(W, 16)
+  QMOE_PK_W(1)
+  QMOE_PK_W(2)
+  QMOE_PK_W(4)
+  QMOE_PK_W(8)
+  QMOE_PK(1, 20)
+  QMOE_PK(2, 20)
+  QMOE_PK(4, 20)
+#undef QMOE_PK_W
+#undef QMOE_PK
+  return fail(QMOE_ERR_INVALID, "qmoe_gemm: packed GEMV needs K in {512, 1024, 2048, 4096}");
+}
+
+template <int MODE>
 static int launch_gemv(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                        void* C, int64_t ldc, hipStream_t s) {
   const size_t shm = size_t(M) * K * 2;
   const int kc = K / 512;
+  if (M >= 2 && M <= 8 && (kc == 1 || kc == 2 || kc == 4 || kc == 8) && int64_t(N) * K * 2 < (1ll << 31))
+    return launch_gemv_pk<MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (M >= 2 && (kc == 1 || kc == 2 || kc == 4 || kc == 8))
     return launch_gemv_mfma<MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (kc == 1 || kc == 2 || kc == 4 || kc == 8) {

@@ -809,23 +809,8 @@ static int check_block_args(const char* fn, const qmoe_bf16* x, const float* h,
   return QMOE_OK;
 }
 
-// Compute units of the current device (read once per device); the fused
-// T = 1 launch needs one resident workgroup per CU for all FB_WGS.
-constexpr int CU_MAX_DEVICES = 64;
-static std::atomic<int> g_cus[CU_MAX_DEVICES];
-
-static int current_device_cus() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= CU_MAX_DEVICES) return 0;
-  int n = g_cus[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    g_cus[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
-// The single-launch form covers one token at the shape it is built for.
+// The single-launch form covers one token at the shape it is built for, with
+// all FB_WGS workgroups resident at once (one per CU).
 static bool fused_block_applies(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
   return T == 1 && H == FB_H && I == FB_I && k == FB_K && E <= ROUTER_MAX_E &&
          current_device_cus() >= FB_WGS;

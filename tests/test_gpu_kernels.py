@@ -42,7 +42,11 @@ def _fp32_reference_matmuls():
                                    # from 224 tiles of 256x256: the 8-wave deep-staged pipeline
                                    # (ragged M and N; the B=8 x 1024 o_proj shape), and the
                                    # 256x256 two-stage one when N % 4 != 0
-                                   (7000, 2052, 512), (8192, 2048, 4096), (7000, 2050, 512)])
+                                   (7000, 2052, 512), (8192, 2048, 4096), (7000, 2050, 512),
+                                   # 2-8 rows, packed-A GEMV: 20 / 16 / 8 / 4 columns per workgroup,
+                                   # 1-8 waves, ragged last workgroup
+                                   (8, 5120, 2048), (2, 5123, 2048), (3, 4100, 1024), (7, 1000, 512),
+                                   (6, 40000, 2048), (4, 2050, 4096)])
 def test_gemm_vs_fp32(dev, M, N, K):
     announce(f"gemm M={M} N={N} K={K}")
     g = torch.Generator(device=dev).manual_seed(M * 7 + N)
