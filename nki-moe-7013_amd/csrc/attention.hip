@@ -1235,11 +1235,16 @@ extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, 
 
 // Waves per split workgroup: four (one merged partial per 256 keys) when the
 // step has many 64-key waves, i.e. the batch x kv heads and the cache
-// capacity are both large; one otherwise.  Chosen from the cache shape, not
-// from max_ctx, so a bucket-sized launch and a full-capacity launch split
-// the keys alike and give the same bits.
+// capacity are both large, or when the cache alone holds 64 or more waves'
+// keys (at batch 1 and context 8000 the merge of 129 one-wave partials per
+// head costs more than the wider splits save: 20.7 -> 13.3 us a step; at
+// context 800 one wave per split stays ahead, 8.8 against 10.2 us); one
+// otherwise.  Chosen from the cache shape, not from max_ctx, so a
+// bucket-sized launch and a full-capacity launch split the keys alike and
+// give the same bits.
 static int ad_subs(int64_t B, int64_t Hkv, int64_t S_max) {
-  return (B * Hkv >= 16 && (S_max + AD_WKEYS - 1) / AD_WKEYS * B * Hkv >= 2048) ? AD_MAX_SUBS : 1;
+  const int64_t waves = (S_max + AD_WKEYS - 1) / AD_WKEYS;
+  return (waves >= 64 || (B * Hkv >= 16 && waves * B * Hkv >= 2048)) ? AD_MAX_SUBS : 1;
 }
 
 // B query rows; chunk_start / qpb as in ad_ctx (nullptr / 1: one query per batch row).

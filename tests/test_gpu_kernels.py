@@ -697,7 +697,9 @@ def test_qkv_finish_matches_qkv_norm_rope(dev, attn_w):
     (1, 32, 4, 2048, [0], None), (1, 32, 4, 2048, [63], 1024), (1, 32, 4, 2048, [64], 1024),
     (3, 32, 4, 2048, [700, 5, 1023], 1024), (2, 32, 2, 512, [100, 511], None), (2, 4, 4, 512, [10, 300], None),
     (8, 32, 4, 8193, [1279, 0, 255, 256, 4000, 8192, 63, 64], None),
-    (3, 32, 4, 2048, [1024, 100, 2047], 1024), (1, 32, 4, 2048, [1500], 256)])
+    (3, 32, 4, 2048, [1024, 100, 2047], 1024), (1, 32, 4, 2048, [1500], 256),
+    # batch 1 over a long cache (four waves per split workgroup), through a bucket too
+    (1, 32, 4, 8193, [8000], None), (2, 32, 4, 8193, [100, 5000], 8192), (1, 32, 4, 8193, [700], 1024)])
 def test_attn_decode_fused_matches_finish_then_decode(dev, B, Hq_, Hkv_, S_max, pos, bucket):
     """qmoe_attn_decode_fused gives the bits of qmoe_qkv_finish followed by the
     decode attention over ctx = position + 1: the same output and the same
