@@ -1151,19 +1151,27 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                            max_p, eps, q_out, k_cache, v_cache, as_stream(stream));
   if (T >= QKV_PIPE_MIN_T && H % 64 == 0 && T * H * 2 < (1ll << 32)) {
     // 256-row tiles once they give every CU a workgroup; below that 128-row
-    // tiles, two per CU, while they fill the CUs; below that 64-row tiles
-    // (a 640-token prompt: 400 workgroups instead of 200)
-    if ((T + 255) / 256 * (Hq + 2 * Hkv) >= 256)
+    // tiles, two per CU, while they fill the CUs.  Fewer tiles than CUs: one
+    // workgroup per CU with four stages in flight, 64-row tiles while those
+    // fit in one round, else 128-row ones (the GEMM alone at N = 5120, K =
+    // 2048: 384 tokens 19.0 -> 17.5 us, 640 tokens 29.4 -> 23.2 us against
+    // 64-row tiles two per CU, which need two rounds from 512 tokens on)
+    const int64_t NH = Hq + 2 * Hkv;
+    if ((T + 255) / 256 * NH >= 256)
       return qkv_pipe_launch<pipe::Pipe<256, 128, 64, 2>, 1>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
                                                               positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
                                                               k_cache, v_cache, as_stream(stream));
-    if ((T + 127) / 128 * (Hq + 2 * Hkv) >= 256)
+    if ((T + 127) / 128 * NH >= 256)
       return qkv_pipe_launch<pipe::Pipe<128, 128, 64, 2>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
                                                               positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
                                                               k_cache, v_cache, as_stream(stream));
-    return qkv_pipe_launch<pipe::Pipe<64, 128, 64, 3>, 2>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
-                                                           positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
-                                                           k_cache, v_cache, as_stream(stream));
+    if ((T + 63) / 64 * NH <= current_device_cus())
+      return qkv_pipe_launch<pipe::Pipe<64, 128, 64, 4>, 1>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                             positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                             k_cache, v_cache, as_stream(stream));
+    return qkv_pipe_launch<pipe::Pipe<128, 128, 64, 4>, 1>(x, wqkv, q_norm_w, k_norm_w, rope_cos, rope_sin,
+                                                            positions, T, S, H, Hq, Hkv, S_max, max_p, eps, q_out,
+                                                            k_cache, v_cache, as_stream(stream));
   }
   dim3 grid(unsigned(Hq + 2 * Hkv), unsigned((T + tile::BM - 1) / tile::BM));
   hipLaunchKernelGGL(qkv_norm_rope_kernel, grid, dim3(256), 0, as_stream(stream), x, wqkv, q_norm_w,

@@ -507,12 +507,13 @@ def _rope(max_pos, dev):
 
 
 # B*S <= 16: GEMV + finish path (8, 16: batched decode steps); up to 255 rows:
-# 128-row MFMA tiles; from 256 rows the direct-to-LDS pipelines: 64-row tiles
-# while 128-row tiles would not fill the CUs (1 x 640, 3 x 130: ragged), then
-# 128-row (3 x 257) and 256-row tiles (3 x 900, 8 x 1000: ragged)
+# 128-row MFMA tiles; from 256 rows the direct-to-LDS pipelines: one
+# workgroup per CU while the tiles fit one round, 64-row tiles (1 x 300, 2 x
+# 180: ragged) or 128-row ones (1 x 640, 3 x 130: ragged), then 128-row
+# tiles two per CU (3 x 257) and 256-row tiles (3 x 900, 8 x 1000: ragged)
 @pytest.mark.parametrize("B,S,start", [(2, 100, 0), (1, 5, 8000), (3, 257, 0), (8, 1, 1279), (16, 1, 40),
                                        (1, 1, 0), (3, 900, 5), (2, 1024, 0), (1, 200, 3), (8, 1000, 3),
-                                       (1, 640, 0), (3, 130, 11)])
+                                       (1, 640, 0), (3, 130, 11), (1, 300, 7), (2, 180, 0)])
 def test_qkv_norm_rope(dev, attn_w, B, S, start):
     announce(f"qkv_norm_rope B={B} S={S} start={start}")
     wqkv, qn, kn = attn_w
