@@ -293,6 +293,18 @@ int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slo
                      const float* topk_w, const float* residual, int64_t T, int64_t k,
                      int64_t H, float* out, qmoe_stream_t stream);
 
+/* qmoe_moe_combine, then the RMSNorm of each finished row:
+ *   x_out[t] = bf16(rms_w * out[t] * rsqrt(mean(out[t]^2) + eps))
+ * (the next decoder layer's input norm), with the bits of qmoe_moe_combine
+ * followed by qmoe_rmsnorm_residual on `out`.  One launch, a workgroup per
+ * token row.  rms_w: bf16 [H]; x_out: bf16 [T, H]; H % 4 == 0, H <= 8192.
+ * Replaces: the MoE output's residual add (qwen_with_nki.py:10207) and the
+ *   next layer's input_layernorm (10185-10189). */
+int qmoe_moe_combine_norm(const void* y_slot, int y_is_bf16, const int32_t* token_slot,
+                          const float* topk_w, const float* residual, int64_t T, int64_t k, int64_t H,
+                          float* out, const qmoe_bf16* rms_w, float eps, qmoe_bf16* x_out,
+                          qmoe_stream_t stream);
+
 /* Dense GEMM C = A . B^T with an epilogue mode (QMOE_GEMM_*); bf16 inputs,
  * fp32 accumulation.  A: bf16 [M, K] (row stride lda); B: bf16 [N, K];
  * C: [M, N] with row stride ldc.  Limits: K % 64 == 0 and A, B below
@@ -303,6 +315,21 @@ int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t* token_slo
  *   _nki_lm_head_kernel 1766-1805. */
 int qmoe_gemm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
               int64_t K, int mode, void* C, int64_t ldc, qmoe_stream_t stream);
+
+/* C += A . B^T (fp32 C[M, N], row stride N), then x_out = bf16(rms_w *
+ * C * rsqrt(mean(C^2 over the row) + eps)) for every row: the o_proj's
+ * residual add and the post-attention RMSNorm of a prefill chunk.  With a
+ * split-K plan and workspace (as qmoe_gemm_ws) the norm runs inside the
+ * launch that adds the slices; otherwise qmoe_gemm then
+ * qmoe_rmsnorm_residual.  Either way the bits of those two calls.
+ *   A: bf16 [M, K] (lda); B: bf16 [N, K]; rms_w: bf16 [N]; x_out: bf16
+ *   [M, N]; N % 4 == 0, N <= 8192.
+ * Replaces: the attention output projection into the residual and the
+ *   post-attention RMSNorm of the decoder layer (qwen_with_nki.py:10200-10205;
+ *   o_proj 10089-10099). */
+int qmoe_gemm_ws_add_rmsnorm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+                             int64_t K, float* C, const qmoe_bf16* rms_w, float eps, qmoe_bf16* x_out,
+                             void* workspace, int64_t workspace_bytes, qmoe_stream_t stream);
 
 /* qmoe_gemm with a caller-owned workspace for split-K: when the problem has
  * too few output tiles to occupy the GPU (prefill-size o_proj, 640 x 2048

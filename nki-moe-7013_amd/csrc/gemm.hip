@@ -11,6 +11,7 @@
 #include "gemm.hpp"
 #include "mfma_pipe.hpp"
 #include "mfma_wide.hpp"
+#include "norm_impl.hpp"
 
 namespace qmoe {
 
@@ -575,6 +576,50 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   store_out<MODE>(C, row * ldc + col + 3, v.w);
 }
 
+// The ADD_F32 reduction of whole rows (one workgroup per row, the chunks of
+// norm_impl.hpp) followed by the row's RMSNorm: C[row] += sum of the slices
+// (splitk_reduce_kernel's order), x_out[row] = bf16(rms_w * C[row] * r).
+__global__ __launch_bounds__(NORM_THREADS) void splitk_reduce_norm_kernel(
+    const float* __restrict__ part, int splits, int M, int N, float* C, const uint16_t* __restrict__ rms_w,
+    float eps, uint16_t* __restrict__ x_out) {
+  const int64_t row = blockIdx.x;
+  const int64_t slab = int64_t(M) * N;
+  float4 v[NORM_MAX_CHUNKS];
+  float ss = 0.0f;
+  const int nchunk = N / 4;
+#pragma unroll
+  for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+    const int c = int(threadIdx.x) + j * NORM_THREADS;
+    if (c < nchunk) {
+      const int64_t o = row * N + 4 * c;
+      float4 a = *reinterpret_cast<const float4*>(part + o);
+      for (int s = 1; s < splits; ++s) {
+        const float4 w = *reinterpret_cast<const float4*>(part + s * slab + o);
+        a.x += w.x;
+        a.y += w.y;
+        a.z += w.z;
+        a.w += w.w;
+      }
+      float4 h = *reinterpret_cast<const float4*>(C + o);
+      h.x += a.x;
+      h.y += a.y;
+      h.z += a.z;
+      h.w += a.w;
+      *reinterpret_cast<float4*>(C + o) = h;
+      v[j] = h;
+      ss += norm_sq4(h);
+    }
+  }
+  __shared__ float red[NORM_THREADS / 64];
+  const float r = norm_rsqrt(ss, N, eps, red);
+  uint16_t* xr = x_out + row * N;
+#pragma unroll
+  for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+    const int c = int(threadIdx.x) + j * NORM_THREADS;
+    if (c < nchunk) reinterpret_cast<uint2*>(xr)[c] = norm_out4(v[j], r, rms_w, c);
+  }
+}
+
 using SplitSmall = pipe::Pipe<128, 128, 64, 2>;
 using SplitMid = pipe::Pipe<64, 128, 64, 3>;
 using SplitTiny = pipe::Pipe<64, 64, 64, 4>;
@@ -607,7 +652,8 @@ static int splitk_plan(int64_t M, int64_t N, int64_t K, SplitTile* tile) {
 
 template <class P, int MODE>
 static int launch_splitk(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K, int splits,
-                         float* part, void* C, int64_t ldc, hipStream_t s) {
+                         float* part, void* C, int64_t ldc, hipStream_t s, const uint16_t* rms_w = nullptr,
+                         float eps = 0.0f, uint16_t* x_out = nullptr) {
   static const bool attr = [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_splitk_kernel<P, 2>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, P::SMEM);
@@ -618,6 +664,11 @@ static int launch_splitk(const uint16_t* A, int64_t lda, const uint16_t* B, int 
   hipLaunchKernelGGL((gemm_splitk_kernel<P, 2>), dim3(unsigned(tiles * splits)), dim3(256), P::SMEM, s, A, lda,
                      B, M, N, K, splits, part);
   if (int rc = hip_status("qmoe_gemm_ws(slices)")) return rc;
+  if (x_out) {  // ADD_F32 into rows of N floats, then their RMSNorm
+    hipLaunchKernelGGL(splitk_reduce_norm_kernel, dim3(unsigned(M)), dim3(NORM_THREADS), 0, s, part, splits, M, N,
+                       static_cast<float*>(C), rms_w, eps, x_out);
+    return hip_status("qmoe_gemm_ws(reduce + norm)");
+  }
   const int64_t n4 = int64_t(M) * (N / 4);
   hipLaunchKernelGGL(splitk_reduce_kernel<MODE>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, s, part, splits,
                      M, N, C, ldc);
@@ -927,4 +978,37 @@ extern "C" int qmoe_gemm_ws(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B,
       QMOE_SPLIT(QMOE_GEMM_ADD_F32)
   }
 #undef QMOE_SPLIT
+}
+
+extern "C" int qmoe_gemm_ws_add_rmsnorm(const qmoe_bf16* A, int64_t lda, const qmoe_bf16* B, int64_t M, int64_t N,
+                                       int64_t K, float* C, const qmoe_bf16* rms_w, float eps, qmoe_bf16* x_out,
+                                       void* workspace, int64_t workspace_bytes, qmoe_stream_t stream) {
+  using namespace qmoe;
+  QMOE_REQUIRE(A && B && C && rms_w && x_out, "qmoe_gemm_ws_add_rmsnorm: null pointer");
+  QMOE_REQUIRE(M >= 0 && M < (1ll << 31) && N > 0 && K > 0, "qmoe_gemm_ws_add_rmsnorm: bad shape");
+  QMOE_REQUIRE(N % 4 == 0 && N <= NORM_THREADS * 4 * NORM_MAX_CHUNKS,
+               "qmoe_gemm_ws_add_rmsnorm: N must be a multiple of 4 and <= 8192 (N=%lld)", (long long)N);
+  QMOE_REQUIRE(eps >= 0.0f, "qmoe_gemm_ws_add_rmsnorm: eps < 0");
+  QMOE_REQUIRE(lda >= K && lda % 8 == 0, "qmoe_gemm_ws_add_rmsnorm: bad lda");
+  if (M == 0) return QMOE_OK;
+  SplitTile tile = SPLIT_TINY;
+  const int splits = splitk_plan(M, N, K, &tile);
+  const int64_t need = splits ? int64_t(splits) * M * N * int64_t(sizeof(float)) : 0;
+  hipStream_t s = as_stream(stream);
+  if (splits == 0 || workspace == nullptr || workspace_bytes < need) {
+    // no split: the GEMM's own epilogue adds into C, then the norm reads it back
+    if (int rc = gemm_launch(A, lda, B, M, N, K, QMOE_GEMM_ADD_F32, C, N, s)) return rc;
+    return qmoe_rmsnorm_residual(C, nullptr, rms_w, M, N, eps, nullptr, x_out, stream);
+  }
+  QMOE_REQUIRE((M - 1) * lda * 2 + K * 2 < (1ll << 31) && N * K * 2 < (1ll << 31),
+               "qmoe_gemm_ws_add_rmsnorm: A or B larger than 2 GiB");
+  float* part = static_cast<float*>(workspace);
+  const uint16_t* w = reinterpret_cast<const uint16_t*>(rms_w);
+  uint16_t* xo = reinterpret_cast<uint16_t*>(x_out);
+  return tile == SPLIT_SMALL ? launch_splitk<SplitSmall, QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K), splits,
+                                                                           part, C, N, s, w, eps, xo)
+         : tile == SPLIT_MID ? launch_splitk<SplitMid, QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K), splits,
+                                                                         part, C, N, s, w, eps, xo)
+                             : launch_splitk<SplitTiny, QMOE_GEMM_ADD_F32>(A, lda, B, int(M), int(N), int(K),
+                                                                          splits, part, C, N, s, w, eps, xo);
 }

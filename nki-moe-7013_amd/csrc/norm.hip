@@ -1,12 +1,9 @@
 // Residual RMSNorm: h = x (+ delta); y = bf16(w * h * rsqrt(mean(h^2) + eps)).
 // One workgroup per row; each thread keeps its float4 chunks in registers so
 // the row is read once.  HBM-bound: 4H (x) [+4H delta] [+4H h] + 2H (y) + 2H (w) bytes.
-#include "common.hpp"
+#include "norm_impl.hpp"
 
 namespace qmoe {
-
-constexpr int NORM_THREADS = 256;
-constexpr int NORM_MAX_CHUNKS = 8;  // H <= 256 * 4 * 8 = 8192
 
 __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_residual_kernel(
     const float* __restrict__ x, const float* __restrict__ delta, const uint16_t* __restrict__ w,
@@ -28,30 +25,19 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_residual_kernel(
         a.x += d.x; a.y += d.y; a.z += d.z; a.w += d.w;
       }
       v[j] = a;
-      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      ss += norm_sq4(a);
     }
   }
   __shared__ float red[NORM_THREADS / 64];
-  ss = wave_sum(ss);
-  if ((t & 63) == 0) red[t >> 6] = ss;
-  __syncthreads();
-  float tot = 0.0f;
-#pragma unroll
-  for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
-  const float r = rsqrtf(tot / float(H) + eps);
+  const float r = norm_rsqrt(ss, H, eps, red);
   float* hr = h_out ? h_out + int64_t(row) * H : nullptr;
   uint16_t* yr = y + int64_t(row) * H;
 #pragma unroll
   for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
     const int c = t + j * NORM_THREADS;
     if (c < nchunk) {
-      const float4 a = v[j];
-      if (hr) reinterpret_cast<float4*>(hr)[c] = a;
-      const uint2 wv = reinterpret_cast<const uint2*>(w)[c];
-      uint2 o;
-      o.x = pack_bf16x2(bf16_lo(wv.x) * (a.x * r), bf16_hi(wv.x) * (a.y * r));
-      o.y = pack_bf16x2(bf16_lo(wv.y) * (a.z * r), bf16_hi(wv.y) * (a.w * r));
-      reinterpret_cast<uint2*>(yr)[c] = o;
+      if (hr) reinterpret_cast<float4*>(hr)[c] = v[j];
+      reinterpret_cast<uint2*>(yr)[c] = norm_out4(v[j], r, w, c);
     }
   }
 }

@@ -53,8 +53,10 @@ PROTOTYPES = {
     "qmoe_moe_experts_gemv": (c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_experts_grouped": (c_int, [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P, P]),
     "qmoe_moe_combine": (c_int, [P, c_int, P, P, P, I64, I64, I64, P, P]),
+    "qmoe_moe_combine_norm": (c_int, [P, c_int, P, P, P, I64, I64, I64, P, P, c_float, P, P]),
     "qmoe_gemm": (c_int, [P, I64, P, I64, I64, I64, c_int, P, I64, P]),
     "qmoe_gemm_ws": (c_int, [P, I64, P, I64, I64, I64, c_int, P, I64, P, I64, P]),
+    "qmoe_gemm_ws_add_rmsnorm": (c_int, [P, I64, P, I64, I64, I64, P, P, c_float, P, P, I64, P]),
     "qmoe_gemm_ws_workspace": (c_int64, [I64, I64, I64]),
     "qmoe_qkv_norm_rope": (
         c_int,

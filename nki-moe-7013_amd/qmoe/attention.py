@@ -93,7 +93,8 @@ class Attention:
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor, B: int, S: int,
                 cache: KVCache, rope_cos: torch.Tensor, rope_sin: torch.Tensor, start=0,
-                max_ctx: Optional[int] = None, norm: Optional[tuple] = None) -> torch.Tensor:
+                max_ctx: Optional[int] = None, norm: Optional[tuple] = None,
+                post_norm: Optional[tuple] = None) -> torch.Tensor:
         """``x[B*S, H]`` bf16 (input-normed), ``residual[B*S, H]`` f32 (updated
         in place), ``positions[B*S]`` i32 (RoPE position == cache index).
 
@@ -105,6 +106,9 @@ class Attention:
         attention launch (``attn_decode_fused``).
         ``norm = (rms_w, eps)``: ``x`` is the fp32 residual row itself (B*S == 1)
         and the input RMSNorm is fused into the QKV GEMV.
+        ``post_norm = (rms_w, eps)``: returns ``bf16(rmsnorm(residual) * rms_w)``
+        of the updated residual, computed with the o_proj's residual add
+        (instead of the residual itself).
         """
         n_ws = ops.qkv_norm_rope_workspace(B * S, x.shape[1], self.n_q, self.n_kv, self.head_dim)
         qws = self._ws.get(("qkv", B * S))
@@ -143,5 +147,7 @@ class Attention:
         key = ("oproj", o.shape[0])
         if key not in self._ws:  # split-K scratch for prefill-size token counts (None: not split)
             self._ws[key] = ops.gemm_workspace(o.shape[0], self.wo.shape[0], self.wo.shape[1], x.device)
+        if post_norm is not None:
+            return ops.gemm_add_rmsnorm(o, self.wo, residual, post_norm[0], post_norm[1], workspace=self._ws[key])
         ops.gemm(o, self.wo, _lib.GEMM_ADD_F32, out=residual, workspace=self._ws[key])
         return residual

@@ -164,19 +164,35 @@ class NeuronQwen3MoeDecoderLayer:
         self._rope = None  # (cos, sin) built from head_dim / rope_theta on first use
 
     def run(self, h: torch.Tensor, positions: torch.Tensor, B: int, S: int, rope, start=0,
-            max_ctx: Optional[int] = None) -> torch.Tensor:
-        """In-place layer on the fp32 residual ``h[B*S, H]``."""
+            max_ctx: Optional[int] = None, x_in: Optional[torch.Tensor] = None,
+            next_norm: Optional[tuple] = None) -> Optional[torch.Tensor]:
+        """In-place layer on the fp32 residual ``h[B*S, H]``.
+
+        Above the decode-block size the RMSNorms ride on the launches that
+        finish their input rows: the post-attention norm on the o_proj's
+        residual add, and, with ``next_norm = (rms_w, eps)`` (the next layer's
+        input norm), that norm on the MoE combine; the latter's bf16 rows are
+        returned for the next layer's ``x_in`` (the bits of a separate
+        ``rmsnorm_residual``).  Otherwise returns None."""
         eps = self.input_layernorm.eps
         if B * S == 1 and ops.qkv_norm_rope_workspace(1, h.shape[1], self.self_attn.n_q, self.self_attn.n_kv,
                                                       self.self_attn.head_dim) > 0:
             # one-token step: the input RMSNorm runs inside the QKV GEMV's staging
             self.self_attn.forward(h, h, positions, B, S, self.cache, rope[0], rope[1], start, max_ctx,
                                    norm=(self.input_layernorm.weight, eps))
-        else:
-            x = ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
+            self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
+            return None
+        x = x_in if x_in is not None else ops.rmsnorm_residual(h, self.input_layernorm.weight, eps)
+        if B * S <= ops.DECODE_BLOCK_MAX_T:
             self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, max_ctx)
-        self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
-        return h
+            self.mlp.forward_normed(h, self.post_attention_layernorm.weight, eps, residual=h, out=h)
+            return None
+        x2 = self.self_attn.forward(x, h, positions, B, S, self.cache, rope[0], rope[1], start, max_ctx,
+                                    post_norm=(self.post_attention_layernorm.weight, eps))
+        if next_norm is None:
+            self.mlp.forward(x2, residual=h, out=h)
+            return None
+        return self.mlp.forward(x2, residual=h, out=h, norm=next_norm)[1]
 
     def rope_tables(self, n_pos: int, device):
         """cos/sin tables covering positions ``[0, n_pos)`` from the config's
@@ -303,8 +319,11 @@ class NeuronQwen3MoeModel:
                h_buf: Optional[torch.Tensor] = None, max_ctx: Optional[int] = None) -> torch.Tensor:
         """fp32 final hidden states ``[B*S, H]`` (before the final norm)."""
         h = ops.embed(input_ids.reshape(-1).long(), self.embed_tokens, out=h_buf, err=self.embed_err)
-        for layer in self.layers:
-            layer.run(h, positions, B, S, self.rope, start, max_ctx)
+        x = None  # the next layer's normed input rows, when the previous layer produced them
+        for i, layer in enumerate(self.layers):
+            nxt = self.layers[i + 1].input_layernorm if i + 1 < len(self.layers) else None
+            x = layer.run(h, positions, B, S, self.rope, start, max_ctx, x_in=x,
+                          next_norm=None if nxt is None else (nxt.weight, nxt.eps))
         return h
 
     def check_embed(self) -> None:

@@ -129,10 +129,14 @@ class MoEBlock:
         self._bufs = {}
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """``residual + MoE(x)`` (fp32) for bf16 ``x[T,H]``."""
+                out: Optional[torch.Tensor] = None, norm: Optional[tuple] = None):
+        """``residual + MoE(x)`` (fp32) for bf16 ``x[T,H]``.  ``norm = (rms_w,
+        eps)`` (above the decode-block size): the combine also normalises the
+        finished rows, and the call returns ``(out, bf16 normed rows)``."""
         T = x.shape[0]
         ex = self.experts
+        if norm is not None and T <= ops.DECODE_BLOCK_MAX_T:
+            raise ValueError("the fused output norm is for T > DECODE_BLOCK_MAX_T")
         if T <= ops.DECODE_BLOCK_MAX_T:
             bufs = self._decode_bufs(T, x.device)
             out = ops.moe_decode_block(self.w_router, ex.w13, ex.w2, self.top_k, x=x, bias=self.router_bias,
@@ -147,7 +151,7 @@ class MoEBlock:
             y = ops.moe_experts_gemv(x, ex.w13, ex.w2, route)
         else:
             y = ops.moe_experts_grouped(x, ex.w13, ex.w2, route)
-        return ops.moe_combine(y, route, route.topk_w, residual, out)
+        return ops.moe_combine(y, route, route.topk_w, residual, out, norm=norm)
 
     def forward_normed(self, h: torch.Tensor, rms_w: torch.Tensor, eps: float,
                        residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):

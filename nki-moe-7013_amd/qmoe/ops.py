@@ -377,8 +377,12 @@ def moe_experts_grouped(
 def moe_combine(
     y_slot: torch.Tensor, route: Route, topk_w: torch.Tensor,
     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-) -> torch.Tensor:
-    """``out[t] = residual[t] + sum_j topk_w[t,j] * y_slot[token_slot[t*k+j]]`` (f32)."""
+    norm: Optional[tuple] = None,
+):
+    """``out[t] = residual[t] + sum_j topk_w[t,j] * y_slot[token_slot[t*k+j]]`` (f32).
+    ``norm = (rms_w, eps)``: also the RMSNorm of every ``out`` row (the bits
+    of :func:`rmsnorm_residual` on ``out``), in the same launch; returns
+    ``(out, x)`` with ``x`` bf16 ``[T, H]``."""
     T, k = route.T, route.k
     if y_slot.dim() != 2 or y_slot.shape[0] != T * k:
         raise ValueError("y_slot must be [T*k, H]")
@@ -392,6 +396,19 @@ def moe_combine(
     out = torch.empty(T, H, dtype=F32, device=y_slot.device) if out is None else out
     _need(out, "out", F32, (T, H))
     _same_device(y_slot, topk_w, residual, out, route.token_slot)
+    if norm is not None:
+        rms_w, eps = norm
+        _need(rms_w, "rms_w", BF16, (H,))
+        x = torch.empty(T, H, dtype=BF16, device=y_slot.device)
+        _same_device(out, rms_w)
+        check(
+            lib().qmoe_moe_combine_norm(
+                _ptr(y_slot), int(y_slot.dtype == BF16), _ptr(route.token_slot), _ptr(topk_w),
+                _ptr(residual), T, k, H, _ptr(out), _ptr(rms_w), float(eps), _ptr(x), _stream(),
+            ),
+            "qmoe_moe_combine_norm",
+        )
+        return out, x
     check(
         lib().qmoe_moe_combine(
             _ptr(y_slot), int(y_slot.dtype == BF16), _ptr(route.token_slot), _ptr(topk_w),
@@ -437,6 +454,31 @@ def gemm(A: torch.Tensor, B: torch.Tensor, mode: int = _lib.GEMM_STORE_BF16,
         return out
     check(lib().qmoe_gemm(_ptr(A), K, _ptr(B), M, N, K, int(mode), _ptr(out), N, _stream()), "qmoe_gemm")
     return out
+
+
+def gemm_add_rmsnorm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, rms_w: torch.Tensor, eps: float,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``C += A . B^T`` (fp32 ``C[M, N]`` in place), then returns
+    ``bf16(rmsnorm(C) * rms_w)``: the bits of :func:`gemm` (ADD_F32) then
+    :func:`rmsnorm_residual`, with the norm inside the split-K reduction
+    when ``workspace`` (from :func:`gemm_workspace`) enables one."""
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
+        raise ValueError("A must be [M,K] and B [N,K]")
+    M, K = A.shape
+    N = B.shape[0]
+    _need(A, "A", BF16)
+    _need(B, "B", BF16)
+    _need(C, "C", F32, (M, N))
+    _need(rms_w, "rms_w", BF16, (N,))
+    x = torch.empty(M, N, dtype=BF16, device=A.device)
+    _same_device(A, B, C, rms_w)
+    if workspace is not None:
+        _need(workspace, "workspace", F32)
+        _same_device(A, workspace)
+    check(lib().qmoe_gemm_ws_add_rmsnorm(_ptr(A), K, _ptr(B), M, N, K, _ptr(C), _ptr(rms_w), float(eps), _ptr(x),
+                                         _ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
+                                         _stream()), "qmoe_gemm_ws_add_rmsnorm")
+    return x
 
 
 def gemv_rmsnorm(h: torch.Tensor, rms_w: torch.Tensor, eps: float, B: torch.Tensor,

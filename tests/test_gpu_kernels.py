@@ -114,6 +114,57 @@ def test_rmsnorm_residual(dev, rows):
         assert float(err.max()) <= 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(640, 2048, 4096), (300, 2048, 1024), (4096, 2048, 512), (33, 516, 256)])
+def test_gemm_add_rmsnorm_bits(dev, M, N, K):
+    """qmoe_gemm_ws_add_rmsnorm (o_proj into the residual + the post-attention
+    norm) gives the bits of qmoe_gemm(ADD_F32) then qmoe_rmsnorm_residual:
+    through the split-K reduction with the norm inside (640 x 2048 x 4096,
+    300 x 2048 x 1024) and through the unsplit fallback (no workspace; a
+    shape that does not split)."""
+    announce(f"gemm_add_rmsnorm M={M} N={N} K={K}")
+    g = torch.Generator(device=dev).manual_seed(M + 3 * N + K)
+    A = bf16_randn((M, K), g, dev)
+    B = bf16_randn((N, K), g, dev, std=0.02)
+    w = bf16_randn((N,), g, dev)
+    h0 = torch.randn(M, N, generator=g, device=dev)
+    ws = ops.gemm_workspace(M, N, K, dev)
+    for workspace in ([ws, None] if ws is not None else [None]):
+        h_ref = h0.clone()
+        ops.gemm(A, B, _lib.GEMM_ADD_F32, out=h_ref, workspace=workspace)
+        x_ref = ops.rmsnorm_residual(h_ref, w, 1e-6)
+        h = h0.clone()
+        x = ops.gemm_add_rmsnorm(A, B, h, w, 1e-6, workspace=workspace)
+        torch.cuda.synchronize()
+        assert torch.equal(h, h_ref) and torch.equal(x, x_ref), f"workspace={workspace is not None}"
+
+
+# top-8 at H = 2048 (the one-pass row form), top-8 at H = 1024 and top-4
+# (the per-chunk forms)
+@pytest.mark.parametrize("T,y_bf16,Hh,kk", [(640, True, 2048, 8), (1000, False, 2048, 8), (9, True, 2048, 8),
+                                            (50, True, 1024, 8), (30, False, 2048, 4)])
+def test_moe_combine_norm_bits(dev, T, y_bf16, Hh, kk):
+    """qmoe_moe_combine_norm (combine + residual, then the next layer's input
+    norm) gives the bits of qmoe_moe_combine then qmoe_rmsnorm_residual, in
+    place on the residual as the layers run it."""
+    announce(f"moe_combine_norm T={T} bf16={y_bf16} H={Hh} k={kk}")
+    g = torch.Generator(device=dev).manual_seed(T + 5)
+    top = torch.from_numpy(_random_topk(T, kk, E, 13 + T)).to(dev)
+    tw = torch.rand(T, kk, generator=g, device=dev)
+    route = ops.moe_permute(top, E, 256)
+    y = torch.randn(T * kk, Hh, generator=g, device=dev)
+    y = y.to(torch.bfloat16) if y_bf16 else y
+    w = bf16_randn((Hh,), g, dev)
+    h0 = torch.randn(T, Hh, generator=g, device=dev)
+    h_ref = h0.clone()
+    ops.moe_combine(y, route, tw, residual=h_ref, out=h_ref)
+    x_ref = ops.rmsnorm_residual(h_ref, w, 1e-6)
+    h = h0.clone()
+    out, x = ops.moe_combine(y, route, tw, residual=h, out=h, norm=(w, 1e-6))
+    torch.cuda.synchronize()
+    assert out is h
+    assert torch.equal(h, h_ref) and torch.equal(x, x_ref)
+
+
 def test_rmsnorm_reference_recipe_on_gpu(dev):
     """The reference's known-answer recipe (nki_custom_rmsnorm.py:182-214),
     at H=512: seed 42, x (256,512), w randn, eps 1e-6, max|diff| < 1e-3."""
