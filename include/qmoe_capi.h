@@ -268,15 +268,20 @@ int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_b
  *   act: bf16 [T*k, I] workspace; y_slot: bf16 [T*k, H].
  *   Work distribution: one persistent workgroup per CU takes (tile, weight
  *   panel) items from per-XCD queues whose counters live in meta[4..21]
- *   (zeroed by the permute; each kernel's last workgroup puts them back to
- *   zero).  Calls that share one meta array must not overlap.
+ *   (zeroed by the permute; the last workgroup puts them back to zero).
+ *   With I % 64 == 0 and act 128-byte aligned both GEMMs run in one launch:
+ *   the workgroups take the gate_up items first and then the down items, a
+ *   down item waiting until its tile's gate_up items are done; word 3 of
+ *   each live tile row counts them (0 from the permute, 0 again once the
+ *   launch completes), and meta[2] gets bit 1 if such a wait ever gave up.
+ *   Calls that share one meta array or tile table must not overlap.
  *   Limits: H % 256 == 0, I % 32 == 0; x, act and one expert's w13 each
  *   below 2 GiB.
  * Replaces: _nki_cte_moe_left_gate_up_kernel qwen_with_nki.py:5341-5369 (left)
  *   and _nki_cte_moe_down_scatter_kernel 4967-5040 (right), dispatched by
  *   _patched_torch_blockwise_matmul_inference 5872-6003. */
 int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13, const qmoe_bf16* w2,
-                             const int32_t* slot_token, const int32_t* tiles,
+                             const int32_t* slot_token, int32_t* tiles,
                              int32_t* meta, int64_t max_tiles, int64_t T, int64_t H,
                              int64_t I, int64_t E, int64_t k, qmoe_bf16* act,
                              qmoe_bf16* y_slot, qmoe_stream_t stream);

@@ -24,10 +24,13 @@
 //   and write whole 16-byte chunks of contiguous output rows.
 //
 // Work distribution: persistent workgroups (one per CU) take (tile, panel)
-// items from per-XCD queues; see the queue helpers below.
+// items from per-XCD queues; see the queue helpers below.  Both GEMMs run in
+// one launch (moe_experts_fused_kernel) when the act rows are whole cache
+// lines, else as two launches.
 #include <atomic>
 
 #include "mfma_wide.hpp"
+
 
 namespace qmoe {
 
@@ -162,11 +165,20 @@ __device__ __forceinline__ uint2 pack4_bf16(float a, float b, float c, float d) 
   return make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
 }
 
-template <class P>
+// 16-byte store written through to memory (device scope), so a workgroup on
+// another XCD that reads the line after a later signal sees it.
+__device__ __forceinline__ void st16_device(void* p, uint4 v) {
+  const u32x4 w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+
+// DEVICE: the act rows are stored with st16_device and the wave waits for
+// its stores to complete (the single-launch form signals the tile after it).
+template <class P, bool DEVICE>
 __device__ __forceinline__ void gateup_tile(const TileJob& job, const uint16_t* __restrict__ x,
                                             const uint16_t* __restrict__ w13,
                                             const int32_t* __restrict__ slot_token, int T, int H, int I,
-                                            uint16_t* __restrict__ act, uint8_t* smem) {
+                                            uint16_t* act, uint8_t* smem) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const pipe::i32x4 ra = pipe::make_rsrc(w13 + int64_t(job.e) * 2 * I * H, uint32_t(int64_t(2) * I * H * 2));
@@ -215,12 +227,17 @@ __device__ __forceinline__ void gateup_tile(const TileJob& job, const uint16_t* 
   const int chunks = units / 8;
   for (int c = threadIdx.x; c < job.rows * chunks; c += P::THREADS) {
     const int r = c / chunks, k = c % chunks;
-    *reinterpret_cast<uint4*>(dst + int64_t(r) * I + k * 8) = *reinterpret_cast<const uint4*>(tl + r * ACT_LD + k * 8);
+    const uint4 v = *reinterpret_cast<const uint4*>(tl + r * ACT_LD + k * 8);
+    if constexpr (DEVICE)
+      st16_device(dst + int64_t(r) * I + k * 8, v);
+    else
+      *reinterpret_cast<uint4*>(dst + int64_t(r) * I + k * 8) = v;
   }
+  if constexpr (DEVICE) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <class P>
-__device__ __forceinline__ void down_tile(const TileJob& job, const uint16_t* __restrict__ act,
+__device__ __forceinline__ void down_tile(const TileJob& job, const uint16_t* act,
                                           const uint16_t* __restrict__ w2, int slots, int H, int I,
                                           uint16_t* __restrict__ y_slot, uint8_t* smem) {
   const int lane = threadIdx.x & 63;
@@ -279,9 +296,9 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_gateup_grouped_kernel(
     const TileJob job = job_of(item, tiles, npanels);
     const int reserve = job.rows <= COLD_MAX_ROWS ? reserve_own(qu, item) : NO_RESERVE;
     if (job.rows <= COLD_MAX_ROWS)
-      gateup_tile<Cold>(job, x, w13, slot_token, T, H, I, act, smem);
+      gateup_tile<Cold, false>(job, x, w13, slot_token, T, H, I, act, smem);
     else
-      gateup_tile<Hot>(job, x, w13, slot_token, T, H, I, act, smem);
+      gateup_tile<Hot, false>(job, x, w13, slot_token, T, H, I, act, smem);
     item = next_item(qu, reserve, smem);
   }
   finish_queue(ctr, meta + META_DONE);
@@ -307,6 +324,81 @@ __global__ __launch_bounds__(Hot::THREADS, 1) void moe_down_grouped_kernel(
   finish_queue(ctr, meta + META_DONE + 1);
 }
 
+// Both GEMMs in one launch.  The workgroups first take gate_up items (queue
+// 0), then down items (queue 1), so the down items of early tiles fill the
+// CUs that the last gate_up items leave idle, and no launch boundary sits
+// between the two.  A down item of tile t reads the act rows of all of
+// tile t's gate_up panels: each gate_up item stores its act rows through to
+// memory (st16_device), waits for them, and only then adds 1 to the tile's
+// counter tiles[4t + 3] (0 from the permute); a down item waits until the
+// counter holds every panel.  No other line of those act rows reaches the
+// reading XCD's L2 before that (rows are whole cache lines: I % 64 == 0 and
+// act 128-byte aligned, checked by the host), so its DMA reads the stored
+// values.  Waits cannot deadlock: a workgroup takes down items only after
+// every gate_up item has been taken, and gate_up items wait for nothing.  A
+// wait still gives up after TILE_WAIT_SPIN polls (it then sets bit 1 of
+// meta[2] and goes on).  The last workgroup to finish sets the queue
+// counters and the tile counters back to zero.
+constexpr int TILE_WAIT_SPIN = 1 << 20;
+
+__device__ __forceinline__ void wait_tile(const int32_t* cnt, int need, int32_t* meta) {
+  if (threadIdx.x < 64) {
+    bool ok = false;
+    for (int n = 0; n < TILE_WAIT_SPIN; ++n) {
+      ok = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need;
+      if (ok) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    if (!ok && threadIdx.x == 0) atomicOr(meta + 2, 2);
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(Hot::THREADS, 1) void moe_experts_fused_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w13, const uint16_t* __restrict__ w2,
+    const int32_t* __restrict__ slot_token, int32_t* tiles, int32_t* meta, int T, int H, int I, int slots,
+    uint16_t* act, uint16_t* __restrict__ y_slot) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int n_tiles = meta[0], np1 = (2 * I + PANEL - 1) / PANEL, np2 = H / PANEL, xcd = xcc_id();
+  {
+    const Queue qu(meta + META_CTR, n_tiles * np1, xcd);
+    for (int item = next_item(qu, NO_RESERVE, smem); item >= 0;) {
+      const TileJob job = job_of(item, tiles, np1);
+      const int reserve = job.rows <= COLD_MAX_ROWS ? reserve_own(qu, item) : NO_RESERVE;
+      if (job.rows <= COLD_MAX_ROWS)
+        gateup_tile<Cold, true>(job, x, w13, slot_token, T, H, I, act, smem);
+      else
+        gateup_tile<Hot, true>(job, x, w13, slot_token, T, H, I, act, smem);
+      __syncthreads();  // every wave's act stores are complete
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(tiles + 4 * (item / np1) + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      item = next_item(qu, reserve, smem);
+    }
+  }
+  {
+    const Queue qu(meta + META_CTR + 8, n_tiles * np2, xcd);
+    for (int item = next_item(qu, NO_RESERVE, smem); item >= 0;) {
+      const TileJob job = job_of(item, tiles, np2);
+      wait_tile(tiles + 4 * (item / np2) + 3, np1, meta);
+      const int reserve = job.rows <= COLD_MAX_ROWS ? reserve_own(qu, item) : NO_RESERVE;
+      if (job.rows <= COLD_MAX_ROWS && I % Cold::BK == 0)
+        down_tile<Cold>(job, act, w2, slots, H, I, y_slot, smem);
+      else
+        down_tile<Hot>(job, act, w2, slots, H, I, y_slot, smem);
+      item = next_item(qu, reserve, smem);
+    }
+  }
+  int* last = reinterpret_cast<int*>(smem);
+  if (threadIdx.x == 0) *last = atomicAdd(meta + META_DONE, 1) == int(gridDim.x) - 1;
+  __syncthreads();
+  if (*last) {  // every other workgroup is done with the counters
+    for (int t = threadIdx.x; t < n_tiles; t += blockDim.x)
+      __hip_atomic_store(tiles + 4 * t + 3, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < 16) atomicExch(meta + META_CTR + threadIdx.x, 0);
+    if (threadIdx.x == 0) atomicExch(meta + META_DONE, 0);
+  }
+}
+
 // Workgroups per grouped launch: one per CU (the kernels need all of a CU's
 // LDS), no more than there are items.
 unsigned grouped_grid(int64_t items) {
@@ -325,7 +417,7 @@ unsigned grouped_grid(int64_t items) {
 
 extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13,
                                         const qmoe_bf16* w2, const int32_t* slot_token,
-                                        const int32_t* tiles, int32_t* meta,
+                                        int32_t* tiles, int32_t* meta,
                                         int64_t max_tiles, int64_t T, int64_t H, int64_t I,
                                         int64_t E, int64_t k, qmoe_bf16* act, qmoe_bf16* y_slot,
                                         qmoe_stream_t stream) {
@@ -347,10 +439,18 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
                               hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(moe_down_grouped_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(moe_experts_fused_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
     return true;
   }();
   (void)attr;
   hipStream_t s = as_stream(stream);
+  if (I % 64 == 0 && reinterpret_cast<uintptr_t>(act) % 128 == 0) {  // act rows are whole cache lines
+    const unsigned g = grouped_grid(max_tiles * std::max<int64_t>((2 * I + PANEL - 1) / PANEL, H / PANEL));
+    hipLaunchKernelGGL(moe_experts_fused_kernel, dim3(g), dim3(Hot::THREADS), SMEM, s, x, w13, w2, slot_token,
+                       tiles, meta, int(T), int(H), int(I), int(T * k), act, y_slot);
+    return hip_status("qmoe_moe_experts_grouped");
+  }
   const unsigned g1 = grouped_grid(max_tiles * ((2 * I + PANEL - 1) / PANEL)), g2 = grouped_grid(max_tiles * (H / PANEL));
   hipLaunchKernelGGL(moe_gateup_grouped_kernel, dim3(g1), dim3(Hot::THREADS), SMEM, s, x, w13, slot_token,
                      tiles, meta, int(T), int(H), int(I), act);

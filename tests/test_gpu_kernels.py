@@ -424,7 +424,41 @@ def test_experts_grouped_route_reuse(dev, experts):
     assert torch.equal(ys[0], fresh[0]) and torch.equal(ys[2], fresh[0])
     assert torch.equal(ys[1], fresh[1]) and torch.equal(ys[3], fresh[1])
     assert not torch.equal(ys[0], ys[1])
-    assert int(route.meta[4:].abs().sum()) == 0
+    assert int(route.meta[4:].abs().sum()) == 0 and int(route.meta[2]) == 0
+    # the one-launch form's per-tile counters (word 3 of each tile row) are back at zero
+    assert int(route.tiles[: int(route.meta[0]), 3].abs().sum()) == 0
+
+
+@pytest.mark.parametrize("T,spread", [(700, "skew"), (640, "crowded"), (4096, "skew"), (96, "uniform")])
+def test_experts_grouped_one_launch_vs_two(dev, experts, T, spread):
+    """Both GEMMs in one launch (down items waiting on their tile's gate_up
+    items) against the two-launch form, which the library takes when act is
+    not 128-byte aligned: the same y_slot bits.  Routings: Zipf-skewed, a
+    prompt whose tokens crowd onto 8 experts (the random-init model's deep
+    layers: 3 tiles each for 8 experts, a few rows for the rest), uniform."""
+    announce(f"grouped experts one launch vs two, T={T} {spread}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(13 + T)
+    x = bf16_randn((T, H), g, dev)
+    if spread == "crowded":
+        rng = np.random.default_rng(T)
+        top = np.stack([rng.permutation(E)[:K_TOP] for _ in range(T)])
+        hot = rng.permutation(E)[:K_TOP]
+        top[: T - 40] = np.stack([rng.permutation(hot) for _ in range(T - 40)])
+        top = torch.from_numpy(top.astype(np.int32)).to(dev)
+    else:
+        top = torch.from_numpy(_random_topk(T, K_TOP, E, 17 + T, skew=1.1 if spread == "skew" else None)).to(dev)
+    route = ops.moe_permute(top, E, 256)
+    n = T * K_TOP * I
+    flat = torch.empty(n + 64, dtype=torch.bfloat16, device=dev)
+    assert flat.data_ptr() % 128 == 0
+    y1 = ops.moe_experts_grouped(x, w13, w2, route, act=flat[:n].view(T * K_TOP, I))
+    y2 = ops.moe_experts_grouped(x, w13, w2, route, act=flat[32:32 + n].view(T * K_TOP, I))  # 64 B off
+    y3 = ops.moe_experts_grouped(x, w13, w2, route, act=flat[:n].view(T * K_TOP, I))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y1).all())
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)
+    assert int(route.meta[2]) == 0 and int(route.tiles[: int(route.meta[0]), 3].abs().sum()) == 0
 
 
 @pytest.mark.parametrize("T", [1, 8, 48, 49, 64, 128])
