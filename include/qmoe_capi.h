@@ -417,6 +417,26 @@ int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_b
                       int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                       int64_t start, float scale, qmoe_bf16* out, qmoe_stream_t stream);
 
+/* qmoe_attn_prefill with a workspace, which lets a launch with fewer query
+ * tiles (B * Hq * ceil(S/128)) than the GPU has CUs split the key range of
+ * its longer tiles over several workgroups (at most one per CU in all); the
+ * last split of a tile to finish merges the partials in split order, so the
+ * result is deterministic (it differs from qmoe_attn_prefill's in rounding).
+ * Larger launches, or a workspace smaller than
+ * qmoe_attn_prefill_workspace(B, S, Hq, D) bytes, run as qmoe_attn_prefill.
+ * The workspace must be zero before its first use; every call leaves its
+ * counters at zero again.  Calls sharing a workspace must not overlap.
+ * Replaces: as qmoe_attn_prefill (qwen_with_nki.py:25-28, 1251). */
+int qmoe_attn_prefill_ws(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                         int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
+                         int64_t start, float scale, void* workspace, int64_t workspace_bytes,
+                         qmoe_bf16* out, qmoe_stream_t stream);
+
+/* Workspace bytes of qmoe_attn_prefill_ws on the current device (-1 for bad
+ * sizes).
+ * Replaces: nothing in the reference (a sizing helper of this library). */
+int64_t qmoe_attn_prefill_workspace(int64_t B, int64_t S, int64_t Hq, int64_t D);
+
 /* qmoe_attn_decode for contexts known to fit a bucket: ctx_len[b] <= max_ctx
  * <= S_max (larger values are clamped to max_ctx).  The launch is sized for
  * max_ctx instead of the cache capacity S_max (the row stride), so a decode

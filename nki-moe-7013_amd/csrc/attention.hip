@@ -420,10 +420,34 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const uint8_t* p) {
 // are DMA'd into the buffers that K(kt+1) and V(kt) just left.  The DMA
 // sources are range-checked buffer loads ending at kv_end, so rows past the
 // visible range read as zeros.
+// Key-split form (kt_split > 0, host-known start): a query tile whose keys
+// span n_kt > kt_split 64-key tiles is split into ceil(n_kt / kt_split) <=
+// AP_MAX_SPLITS workgroups over consecutive key ranges, so a small grid (a
+// batch-1 prompt) fills the GPU and its longest chain of key steps shortens.
+// Each split stores its unnormalised partial (m, l, O) through to memory
+// (ap_st16), waits for the stores and adds 1 to the tile's counter; the
+// split that counts in last merges the partials in split order (its own
+// from registers), writes the output and sets the counter back to zero.
+// Partial records sit at the workgroup's grid index.  (Counting arrivals
+// first, so the last split skips its own store, was slower: the stores of
+// the others then start a round trip later.)
+struct ApSplit {
+  int kt_split;   // 0: every query tile in one workgroup
+  float* part;    // [gridDim.x][AP_PREC]
+  int32_t* cnt;   // [B * Hq * n_qt], zero between calls
+};
+constexpr int AP_PREC = 2 * AP_QT + AP_QT * HD;  // m[128], l[128], O (fp32, register order)
+constexpr int AP_MAX_SPLITS = 2;  // key splits per query tile
+
+__device__ __forceinline__ void ap_st16(float* p, float a, float b, float c, float d) {
+  const f32x4 w = {a, b, c, d};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+
 __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache,
-    const uint16_t* __restrict__ v_cache, int S, int Hq, int Hkv, int S_max, int start,
-    const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ v_cache, int B, int S, int Hq, int Hkv, int S_max, int start,
+    const int32_t* __restrict__ start_dev, float scale_log2, uint16_t* __restrict__ out, ApSplit sp) {
   if (start_dev) start = min(max(start_dev[0], 0), S_max - S);
   __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * AP_TILE];  // K0, K1, V0, V1
   const int t = threadIdx.x, lane = t & 63;
@@ -434,9 +458,21 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   // heads sharing a kv head sit B * Hkv items apart, i.e. on one XCD when
   // B * Hkv is a multiple of 8 (workgroup i runs on XCD i % 8), whose L2
   // then serves their K/V tiles.
-  const int n_qt = (S + AP_QT - 1) / AP_QT, G = Hq / Hkv, n_grp = int(gridDim.x) / n_qt / G;
-  const int qt = n_qt - 1 - int(blockIdx.x) / (n_grp * G);
-  const int r_band = int(blockIdx.x) % (n_grp * G), grp = r_band % n_grp;
+  const int n_qt = (S + AP_QT - 1) / AP_QT, G = Hq / Hkv, n_grp = B * Hkv;
+  // query tile, key split (bands of ns(qt) * B * Hq workgroups, latest tile first)
+  auto n_kt_of = [&](int t) { return (start + min((t + 1) * AP_QT, S) + AP_KT - 1) / AP_KT; };
+  auto ns_of = [&](int t) { return sp.kt_split > 0 ? (n_kt_of(t) + sp.kt_split - 1) / sp.kt_split : 1; };
+  int qt = n_qt - 1 - int(blockIdx.x) / (n_grp * G), rem = int(blockIdx.x) % (n_grp * G), band0 = 0;
+  if (sp.kt_split > 0) {  // a few bands (the host splits small grids only)
+    qt = n_qt - 1;
+    rem = int(blockIdx.x);
+    for (; qt > 0 && rem >= ns_of(qt) * n_grp * G; --qt) {
+      rem -= ns_of(qt) * n_grp * G;
+      band0 += ns_of(qt) * n_grp * G;
+    }
+  }
+  const int ns = ns_of(qt), split = rem / (n_grp * G);
+  const int r_band = rem % (n_grp * G), grp = r_band % n_grp;
   const int kvh = grp % Hkv, b = grp / Hkv, h = kvh * G + r_band / n_grp;
   const int q0 = qt * AP_QT;
   const int qrow = q0 + wave * 32 + (lane & 31);  // this lane's query (column of S^T)
@@ -468,7 +504,10 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   float m_run = -INFINITY, l_run = 0.0f;
   const int q_idx = start + qrow;               // cache index of this query
   const int kv_end = start + min(q0 + AP_QT, S);  // keys [0, kv_end) can be visible
-  const int n_kt = (kv_end + AP_KT - 1) / AP_KT;
+  // this workgroup's key tiles: [kt0, kt0 + n_kt) of the query tile's
+  const int kt0 = ns > 1 ? split * sp.kt_split : 0;
+  const int n_kt = ns > 1 ? min(sp.kt_split, (kv_end + AP_KT - 1) / AP_KT - kt0) : (kv_end + AP_KT - 1) / AP_KT;
+  const int kv_hi = ns > 1 ? min(kv_end, (kt0 + n_kt) * AP_KT) : kv_end;  // keys the DMA may read
   // keys this wave can see: [0, wave_last]; a tile that ends at or below
   // wave_first is visible to every query of the wave (no mask)
   const int wave_first = start + q0 + wave * 32;
@@ -479,8 +518,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   // instructions of 4 rows (1 KB of LDS each); lane j fills slot j % 16 of row
   // 16w + 4i + j / 16, so it fetches the chunk whose swizzled slot that is
   // (both swizzles are XOR involutions).
-  const pipe::i32x4 rk = pipe::make_rsrc(k_cache + kv_base, uint32_t(kv_end) * AP_ROWB);
-  const pipe::i32x4 rv = pipe::make_rsrc(v_cache + kv_base, uint32_t(kv_end) * AP_ROWB);
+  const int64_t kv_lo = kv_base + int64_t(kt0) * AP_KT * HD;
+  const pipe::i32x4 rk = pipe::make_rsrc(k_cache + kv_lo, uint32_t(kv_hi - kt0 * AP_KT) * AP_ROWB);
+  const pipe::i32x4 rv = pipe::make_rsrc(v_cache + kv_lo, uint32_t(kv_hi - kt0 * AP_KT) * AP_ROWB);
   uint32_t koff[4], voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -638,7 +678,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
   // previous barrier, have landed, and the barrier makes them visible and
   // frees K(kt+1)'s and V(kt)'s buffers.
   auto one = [&](int kt, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next) {
-    const int kv0 = kt * AP_KT, buf = kt & 1;
+    const int kv0 = (kt0 + kt) * AP_KT, buf = kt & 1;
     if constexpr (decltype(has_next)::value) qk(buf ^ 1, nxt);
     if (kv0 <= wave_last) softmax_pv(buf, kv0, cur);  // past this wave's queries: nothing (wave-uniform)
     pipe::wait_vm<0>();
@@ -661,8 +701,89 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
+  if (ns > 1) {
+    // partial of this split -> memory; the split that counts in last merges
+    const int qloc = wave * 32 + (lane & 31);
+    float* rec = sp.part + int64_t(blockIdx.x) * AP_PREC;
+    if (hl == 0) {
+      __hip_atomic_store(rec + qloc, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(rec + AP_QT + qloc, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // O in register order: chunk (wave, db, g) of 64 lanes x 16 bytes, so each
+    // store (and the merging workgroup's load) covers 1 KB of contiguous memory
+    float* ob = rec + 2 * AP_QT + (wave * 16 * 64 + lane) * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        ap_st16(ob + (db * 4 + g) * 256, o[db][g * 4], o[db][g * 4 + 1], o[db][g * 4 + 2], o[db][g * 4 + 3]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave's partial is in memory (and the K/V tiles are free)
+    int* s_last = reinterpret_cast<int*>(smem);
+    int32_t* cnt = sp.cnt + (int64_t(b) * Hq + h) * n_qt + qt;
+    if (t == 0) *s_last = atomicAdd(cnt, 1) == ns - 1;
+    __syncthreads();
+    if (!*s_last) return;
+    if (t == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto rec_of = [&](int j) { return sp.part + int64_t(band0 + j * n_grp * G + r_band) * AP_PREC; };
+    // every other split's (m, l, O) requested at once (ns <= AP_MAX_SPLITS),
+    // then combined in split order
+    float mj[AP_MAX_SPLITS], lj[AP_MAX_SPLITS];
+    float4 oj[AP_MAX_SPLITS][16];
+#pragma unroll
+    for (int j = 0; j < AP_MAX_SPLITS; ++j) {
+      if (j < ns && j != split) {
+        const float* rj = rec_of(j);
+        mj[j] = rj[qloc];
+        lj[j] = rj[AP_QT + qloc];
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            oj[j][db * 4 + g] = *reinterpret_cast<const float4*>(rj + 2 * AP_QT + (wave * 16 * 64 + lane) * 4 +
+                                                                 (db * 4 + g) * 256);
+      } else {
+        mj[j] = j == split ? m_run : -INFINITY;
+        lj[j] = j == split ? l_run : 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            oj[j][db * 4 + g] = j == split ? make_float4(o[db][g * 4], o[db][g * 4 + 1], o[db][g * 4 + 2],
+                                                         o[db][g * 4 + 3])
+                                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < AP_MAX_SPLITS; ++j) M = fmaxf(M, mj[j]);
+    float L = 0.0f;
+    f32x16 acc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < AP_MAX_SPLITS; ++j) {  // split order, whichever split counted in last
+      const float w = mj[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mj[j] - M);
+      L += w * lj[j];
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 v = oj[j][db * 4 + g];
+          acc[db][g * 4] += w * v.x;
+          acc[db][g * 4 + 1] += w * v.y;
+          acc[db][g * 4 + 2] += w * v.z;
+          acc[db][g * 4 + 3] += w * v.w;
+        }
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = acc[db];
+    l_run = L;
+  }
   if (qrow >= S) return;
-  const float inv = 1.0f / l_run;
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   uint16_t* op = out + ((int64_t(b) * S + qrow) * Hq + h) * HD;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -1200,40 +1321,95 @@ extern "C" int qmoe_qkv_finish(const float* qkv, const qmoe_bf16* q_norm_w, cons
   return hip_status("qmoe_qkv_finish");
 }
 
+namespace qmoe {
+// Key splits of the prefill launch: the smallest kt_split (64-key tiles per
+// workgroup, at least 2) whose split grid still fits one workgroup per CU,
+// for grids below the CU count with a host-known start, when it takes at
+// least AP_SPLIT_MIN_GAIN key steps off the longest tile (a split costs
+// about three steps: the partial's store, the count and the merge); 0 (no
+// split) otherwise.  *grid gets the launch's workgroup count.
+constexpr int AP_SPLIT_MIN_GAIN = 4;
+static int ap_kt_split(int64_t B, int64_t S, int64_t Hq, int64_t start, bool host_start, int64_t* grid) {
+  const int64_t n_qt = (S + AP_QT - 1) / AP_QT, base = n_qt * Hq * B, cus = current_device_cus();
+  *grid = base;
+  if (!host_start || base >= cus) return 0;
+  auto n_kt = [&](int64_t t) { return (start + std::min((t + 1) * AP_QT, S) + AP_KT - 1) / AP_KT; };
+  for (int64_t spt = 2; spt <= n_kt(n_qt - 1) - AP_SPLIT_MIN_GAIN; ++spt) {
+    int64_t total = 0;
+    for (int64_t t = 0; t < n_qt; ++t) total += (n_kt(t) + spt - 1) / spt * Hq * B;
+    if (total <= cus && (n_kt(n_qt - 1) + spt - 1) / spt <= AP_MAX_SPLITS) {
+      *grid = total;
+      return int(spt);
+    }
+  }
+  return 0;
+}
+
+// Counter bytes at the head of the prefill workspace (256-byte aligned).
+static int64_t ap_cnt_bytes(int64_t B, int64_t S, int64_t Hq) {
+  return ((S + AP_QT - 1) / AP_QT * Hq * B * 4 + 255) / 256 * 256;
+}
+
+static int ap_launch(const char* fn, const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                     int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, int64_t start,
+                     const int32_t* start_dev, float scale, void* ws, int64_t ws_bytes, qmoe_bf16* out,
+                     qmoe_stream_t stream) {
+  QMOE_REQUIRE(q && k_cache && v_cache && out, "%s: null pointer", fn);
+  QMOE_REQUIRE(D == HD, "%s: head_dim must be 128", fn);
+  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "%s: bad heads", fn);
+  QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max && start >= 0 && start + S <= S_max,
+               "%s: need 0 <= start and start + S <= S_max", fn);
+  QMOE_REQUIRE(S_max <= AP_MAX_SMAX, "%s: S_max must be <= %d", fn, AP_MAX_SMAX);
+  QMOE_REQUIRE(ws_bytes >= 0 && (ws != nullptr || ws_bytes == 0), "%s: bad workspace", fn);
+  if (B == 0 || S == 0) return QMOE_OK;
+  QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "%s: grid too large", fn);
+  int64_t grid = 0;
+  ApSplit sp{0, nullptr, nullptr};
+  if (ws) {
+    const int kt_split = ap_kt_split(B, S, Hq, start, start_dev == nullptr, &grid);
+    const int64_t cb = ap_cnt_bytes(B, S, Hq);
+    if (kt_split > 0 && ws_bytes >= cb + grid * AP_PREC * 4) {
+      sp.kt_split = kt_split;
+      sp.cnt = static_cast<int32_t*>(ws);
+      sp.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + cb);
+    }
+  }
+  if (sp.kt_split == 0) grid = (S + AP_QT - 1) / AP_QT * Hq * B;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(unsigned(grid)), dim3(256), 0, as_stream(stream), q, k_cache,
+                     v_cache, int(B), int(S), int(Hq), int(Hkv), int(S_max), int(start), start_dev, scale_log2,
+                     out, sp);
+  return hip_status(fn);
+}
+}  // namespace qmoe
+
 extern "C" int qmoe_attn_prefill(const qmoe_bf16* q, const qmoe_bf16* k_cache,
                                  const qmoe_bf16* v_cache, int64_t B, int64_t S, int64_t Hq,
                                  int64_t Hkv, int64_t D, int64_t S_max, int64_t start, float scale,
                                  qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && out, "qmoe_attn_prefill: null pointer");
-  QMOE_REQUIRE(D == HD, "qmoe_attn_prefill: head_dim must be 128");
-  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill: bad heads");
-  QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && start >= 0 && start + S <= S_max,
-               "qmoe_attn_prefill: need 0 <= start and start + S <= S_max");
-  QMOE_REQUIRE(S_max <= AP_MAX_SMAX, "qmoe_attn_prefill: S_max must be <= %d", AP_MAX_SMAX);
-  if (B == 0 || S == 0) return QMOE_OK;
-  QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill: grid too large");
-  const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
-  const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
-                     int(S), int(Hq), int(Hkv), int(S_max), int(start), nullptr, scale_log2, out);
-  return hip_status("qmoe_attn_prefill");
+  return qmoe::ap_launch("qmoe_attn_prefill", q, k_cache, v_cache, B, S, Hq, Hkv, D, S_max, start, nullptr, scale,
+                         nullptr, 0, out, stream);
+}
+
+extern "C" int64_t qmoe_attn_prefill_workspace(int64_t B, int64_t S, int64_t Hq, int64_t D) {
+  if (B < 0 || S < 0 || Hq <= 0 || D != qmoe::HD) return -1;
+  return qmoe::ap_cnt_bytes(B, S, Hq) + int64_t(qmoe::current_device_cus()) * qmoe::AP_PREC * 4;
+}
+
+extern "C" int qmoe_attn_prefill_ws(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
+                                    int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
+                                    int64_t start, float scale, void* workspace, int64_t workspace_bytes,
+                                    qmoe_bf16* out, qmoe_stream_t stream) {
+  return qmoe::ap_launch("qmoe_attn_prefill_ws", q, k_cache, v_cache, B, S, Hq, Hkv, D, S_max, start, nullptr,
+                         scale, workspace, workspace_bytes, out, stream);
 }
 
 extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
                                     int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                                     const int32_t* start, float scale, qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && start && out, "qmoe_attn_prefill_at: null pointer");
-  QMOE_REQUIRE(D == HD, "qmoe_attn_prefill_at: head_dim must be 128");
-  QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "qmoe_attn_prefill_at: bad heads");
-  QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max, "qmoe_attn_prefill_at: need S <= S_max");
-  QMOE_REQUIRE(S_max <= AP_MAX_SMAX, "qmoe_attn_prefill_at: S_max must be <= %d", AP_MAX_SMAX);
-  if (B == 0 || S == 0) return QMOE_OK;
-  QMOE_REQUIRE((S + AP_QT - 1) / AP_QT * Hq * B < (1ll << 31), "qmoe_attn_prefill_at: grid too large");
-  const dim3 grid(unsigned((S + AP_QT - 1) / AP_QT * Hq * B));
-  const float scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_prefill_kernel, grid, dim3(256), 0, as_stream(stream), q, k_cache, v_cache,
-                     int(S), int(Hq), int(Hkv), int(S_max), 0, start, scale_log2, out);
-  return hip_status("qmoe_attn_prefill_at");
+  QMOE_REQUIRE(start, "qmoe_attn_prefill_at: null pointer");
+  return qmoe::ap_launch("qmoe_attn_prefill_at", q, k_cache, v_cache, B, S, Hq, Hkv, D, S_max, 0, start, scale,
+                         nullptr, 0, out, stream);
 }
 
 extern "C" int64_t qmoe_attn_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t S_max) {

@@ -65,6 +65,8 @@ PROTOTYPES = {
     "qmoe_qkv_norm_rope_workspace": (c_int64, [I64, I64, I64, I64, I64]),
     "qmoe_attn_prefill": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, I64, c_float, P, P]),
     "qmoe_attn_prefill_at": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, P, c_float, P, P]),
+    "qmoe_attn_prefill_ws": (c_int, [P, P, P, I64, I64, I64, I64, I64, I64, I64, c_float, P, I64, P, P]),
+    "qmoe_attn_prefill_workspace": (c_int64, [I64, I64, I64, I64]),
     "qmoe_attn_decode_workspace": (c_int64, [I64, I64, I64, I64]),
     "qmoe_embed": (c_int, [P, I64, I64, P, I64, P, P, P]),
     "qmoe_argmax": (c_int, [P, I64, I64, I64, P, I64, P, P]),

@@ -140,7 +140,13 @@ class Attention:
                 o = ops.attn_decode_chunk(q.view(B * S, self.n_q, self.head_dim), cache.k, cache.v, B, S, start,
                                           self.scale, ws)
             elif S > 1:
-                o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale)
+                aws = None
+                if not isinstance(start, torch.Tensor):
+                    aws = self._ws.get(("prefill", B, S))
+                    if aws is None:
+                        aws = ops.attn_prefill_workspace(B, S, self.n_q, self.head_dim, x.device)
+                        self._ws[("prefill", B, S)] = aws
+                o = ops.attn_prefill(q, cache.k, cache.v, B, S, start, self.scale, workspace=aws)
             else:
                 o = ops.attn_decode(q.view(B, self.n_q, self.head_dim), cache.k, cache.v, positions + 1, self.scale,
                                     self._decode_ws(B, cache, x.device), max_ctx=max_ctx)

@@ -587,13 +587,23 @@ def qkv_norm_rope_workspace(T: int, H: int, Hq: int, Hkv: int, D: int) -> int:
     return int(lib().qmoe_qkv_norm_rope_workspace(T, H, Hq, Hkv, D))
 
 
+def attn_prefill_workspace(B: int, S: int, Hq: int, D: int, device) -> torch.Tensor:
+    """Zeroed workspace for :func:`attn_prefill` (key-split launches)."""
+    n = int(lib().qmoe_attn_prefill_workspace(B, S, Hq, D))
+    if n < 0:
+        raise ValueError("bad sizes for the prefill attention workspace")
+    return torch.zeros(max(n, 4) // 4, dtype=I32, device=device)
+
+
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, B: int, S: int,
                  start=0, scale: Optional[float] = None,
-                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal GQA attention of ``q[B*S, Hq, D]`` against the cache; returns ``[B*S, Hq*D]``.
     ``start`` (cache index of the first query) is an int, or an int32 ``[1]``
     device tensor read by the kernel (clamped into ``[0, S_max - S]``), so a
-    captured graph replays the call at any position."""
+    captured graph replays the call at any position.  ``workspace`` (from
+    :func:`attn_prefill_workspace`, host ``start`` only) lets a small launch
+    split its longer query tiles' key ranges over more workgroups."""
     T, Hq, D = q.shape
     if T != B * S:
         raise ValueError("q must be [B*S, Hq, D]")
@@ -616,6 +626,17 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         )
         return out
     _same_device(q, k_cache, v_cache, out)
+    if workspace is not None:
+        _same_device(q, workspace)
+        if not workspace.is_contiguous():
+            raise ValueError("workspace must be contiguous")
+        check(
+            lib().qmoe_attn_prefill_ws(_ptr(q), _ptr(k_cache), _ptr(v_cache), B, S, Hq, Hkv, D, S_max,
+                                       start, float(scale), _ptr(workspace), _nbytes(workspace), _ptr(out),
+                                       _stream()),
+            "qmoe_attn_prefill_ws",
+        )
+        return out
     check(
         lib().qmoe_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), B, S, Hq, Hkv, D, S_max,
                                 start, float(scale), _ptr(out), _stream()),

@@ -676,6 +676,39 @@ def test_attn_prefill(dev, B, S, start):
                        max_abs_tol=2e-2, mean_rel_tol=5e-3)
 
 
+@pytest.mark.parametrize("B,S,start", [(1, 640, 0), (1, 512, 0), (1, 300, 0), (1, 440, 200), (2, 256, 0),
+                                       (1, 1024, 0), (1, 64, 0)])
+def test_attn_prefill_key_split(dev, B, S, start):
+    """The workspace form: launches with fewer query tiles than CUs split
+    their longer tiles' key ranges over two workgroups and merge the
+    partials in the tile's last workgroup (640 and 512 tokens, and 440 at
+    start 200, split; the others run unsplit).  Against the oracle, the same
+    bits on a repeat call (split order, not arrival order), close to the
+    unsplit launch, counters back at zero, NaN-poisoned rows unread."""
+    announce(f"attn_prefill key split B={B} S={S} start={start}")
+    S_max = start + S + 17
+    g = torch.Generator(device=dev).manual_seed(3 * S + start + B)
+    q = bf16_randn((B * S, HQ, D), g, dev)
+    kc = bf16_randn((B, HKV, S_max, D), g, dev)
+    vc = bf16_randn((B, HKV, S_max, D), g, dev)
+    kc[:, :, start + S :] = float("nan")
+    vc[:, :, start + S :] = float("nan")
+    ws = ops.attn_prefill_workspace(B, S, HQ, D, dev)
+    out = ops.attn_prefill(q, kc, vc, B, S, start, workspace=ws)
+    out2 = ops.attn_prefill(q, kc, vc, B, S, start, workspace=ws)
+    plain = ops.attn_prefill(q, kc, vc, B, S, start)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    n_cnt = -(-S // 128) * HQ * B
+    assert int(ws[:n_cnt].abs().sum()) == 0
+    assert max_abs(out.float(), plain.float()) < 2e-2
+    qi = (start + torch.arange(S)).view(1, S).expand(B, S)
+    ref = oracle.gqa_attention(q.cpu().view(B, S, HQ, D).transpose(1, 2),
+                               kc.cpu()[:, :, : start + S], vc.cpu()[:, :, : start + S], qi)
+    assert_close_layer(out.cpu().view(B, S, HQ, D), ref, f"attn_prefill split B={B} S={S}",
+                       max_abs_tol=2e-2, mean_rel_tol=5e-3)
+
+
 def test_attention_layer_B8_prefill1024_decode_to_8192(dev, attn_w):
     """The attention-layer workload: batch 8, a 1024-token prefill into a
     cache of 8193 rows, decode steps right after it (positions 1024, 1025),
