@@ -75,8 +75,11 @@ typedef void* qmoe_stream_t;
 
 /* ABI version qmoe_version() returns.  2: the dispatch meta array holds
  * QMOE_META_INTS ints (was 4), and decode-block workspaces start with
- * QMOE_DECODE_BLOCK_STATE_BYTES of call-to-call state (zeroed before first use). */
-#define QMOE_VERSION 2
+ * QMOE_DECODE_BLOCK_STATE_BYTES of call-to-call state (zeroed before first use).
+ * 3: qmoe_moe_experts_grouped takes the tile table non-const (word 3 of each
+ * live row counts finished gate_up panels during the call), and
+ * qmoe_attn_prefill_ws / qmoe_attn_prefill_workspace are new. */
+#define QMOE_VERSION 3
 
 int qmoe_version(void);
 const char* qmoe_last_error(void);

@@ -1,7 +1,6 @@
 // Dispatch-metadata construction inside one workgroup of NT threads
 // (NT in {256, 1024}): histogram, exclusive scans, active-expert list, row-tile
-// table and the stable permutation.  Shared by the stand-alone permute kernel
-// and the fused small-T routing kernel.
+// table and the stable permutation, for the single-workgroup permute kernel.
 //
 // Placement is deterministic and stable: pairs s = t*k + j are processed in
 // chunks of NT in order; inside a wave the rank of a pair among the lanes

@@ -22,7 +22,7 @@ GEMM_ADD_F32 = 2
 W13_GROUP = 32
 W2_BLOCK = 8
 GROUPED_MAX_TILE_M = 256
-VERSION = 2
+VERSION = 3
 META_INTS = 24
 DECODE_BLOCK_WGS = 256
 DECODE_BLOCK_NOALLOC_MAX_TH = 16384

@@ -197,7 +197,7 @@ def moe_permute(topk_idx: torch.Tensor, E: int, tile_m: int = 128, route: Option
 
 def moe_route(x: torch.Tensor, w_router: torch.Tensor, k: int, bias: Optional[torch.Tensor] = None,
               tile_m: int = 128, route: Optional[Route] = None) -> Route:
-    """Router + top-k + dispatch metadata (one launch for T <= 64)."""
+    """Router + top-k + dispatch metadata (qmoe_moe_route_ws)."""
     T, H = x.shape
     E = w_router.shape[0]
     _need(x, "x", BF16)

@@ -45,7 +45,7 @@ def test_header_constants_match_python_mirror():
 
 
 def test_version():
-    assert _lib.lib().qmoe_version() == _lib.VERSION == 2
+    assert _lib.lib().qmoe_version() == _lib.VERSION == 3
 
 
 def test_route_meta_length_checked():

@@ -985,10 +985,12 @@ def test_attn_decode(dev, ctx):
 
 
 # --------------------------------------------------------------------------- fused decode path
-@pytest.mark.parametrize("T", [1, 3, 8, 17, 64, 65, 300])
+@pytest.mark.parametrize("T", [1, 3, 8, 17, 64, 65, 300, 640, 1024, 1025])
 def test_moe_route_fused(dev, router_w, T):
-    """qmoe_moe_route (one launch for T <= 64) == router_topk + permute, on
-    three calls in a row into the same buffers."""
+    """qmoe_moe_route == router_topk + permute, on three calls in a row into
+    the same buffers: the oracle's routing where the gap allows, the
+    oracle's permutation of the ids it chose, the same bits as the two-step
+    path, and the work counters back at zero."""
     announce(f"moe_route T={T}")
     g = torch.Generator(device=dev).manual_seed(500 + T)
     x = bf16_randn((T, H), g, dev)
@@ -1007,6 +1009,17 @@ def test_moe_route_fused(dev, router_w, T):
         assert torch.equal(route.offsets.cpu(), torch.from_numpy(ref["offsets"]))
         n_act = int(route.meta[1])
         assert torch.equal(route.active.cpu()[:n_act], torch.from_numpy(ref["active"]))
+        assert int(route.meta[2]) == 0 and int(route.meta[4:].abs().sum()) == 0
+    # the two-step path on the same logits: router_topk, then moe_permute
+    logits, tw, ti = ops.router_topk(x, router_w, K_TOP)
+    two = ops.moe_permute(ti, E, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(route.logits, logits) and torch.equal(route.topk_idx, ti) and torch.equal(route.topk_w, tw)
+    for f in ("counts", "offsets", "slot_token", "token_slot"):
+        assert torch.equal(getattr(route, f), getattr(two, f)), f
+    n_t, n_act = int(two.meta[0]), int(two.meta[1])
+    assert torch.equal(route.meta[:3], two.meta[:3]) and torch.equal(route.tiles[:n_t], two.tiles[:n_t])
+    assert torch.equal(route.active[:n_act], two.active[:n_act])
 
 
 @pytest.mark.parametrize("T", [1, 2, 5, 8])
