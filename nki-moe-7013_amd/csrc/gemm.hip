@@ -13,6 +13,12 @@
 #include "mfma_wide.hpp"
 #include "norm_impl.hpp"
 
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace qmoe {
 
 template <int MODE>
@@ -488,6 +494,85 @@ static int launch_wide(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
 // with two workgroups per CU; problems that would still leave most CUs idle
 // (the prefill router: 4096 x 128 x 2048) take 64x64 tiles with four stages
 // in flight, since each of their few workgroups walks a long K.
+// Large fp32-output GEMMs (the 8-wave pipeline's sizes, K >= 2048: the
+// batch-8 prompt's o_proj, 8192 x 2048 x 4096) go to hipBLASLt, a plain
+// library GEMM: C (fp32, ldc) = A . B^T (+ C with ADD_F32).  It keeps the
+// long-K tiles' MFMA rate and overlaps the fp32 C read-modify-write that the
+// one-tile-per-CU pipeline leaves to the end (8192 x 2048 x 4096: 103 us
+// against 145-155 us).  One handle per device, one plan per shape (the
+// heuristic's first algorithm, no workspace); a shape the library has no
+// algorithm for stays on the pipeline.
+namespace {
+struct BltPlan {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool ok = false;
+};
+std::mutex blt_mu;
+std::map<int, hipblasLtHandle_t> blt_handles;
+std::map<std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t>, BltPlan> blt_plans;
+
+const BltPlan* blt_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc, hipblasLtHandle_t* h) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> g(blt_mu);
+  auto hi = blt_handles.find(dev);
+  if (hi == blt_handles.end()) {
+    hipblasLtHandle_t nh = nullptr;
+    if (hipblasLtCreate(&nh) != HIPBLAS_STATUS_SUCCESS) nh = nullptr;
+    hi = blt_handles.emplace(dev, nh).first;
+  }
+  if (!hi->second) return nullptr;
+  *h = hi->second;
+  auto key = std::make_tuple(dev, M, N, K, lda, ldc);
+  auto pi = blt_plans.find(key);
+  if (pi != blt_plans.end()) return pi->second.ok ? &pi->second : nullptr;
+  BltPlan p;
+  // column-major view: C^T (N x M, ld ldc) = B (N x K row-major = K x N, op T) . A^T (K x M, ld lda)
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  bool ok = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+                HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+                HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, uint64_t(K), uint64_t(N), K) == HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, uint64_t(K), uint64_t(M), lda) == HIPBLAS_STATUS_SUCCESS &&
+            hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, uint64_t(N), uint64_t(M), ldc) == HIPBLAS_STATUS_SUCCESS;
+  if (ok) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    uint64_t wsb = 0;
+    hipblasLtMatmulHeuristicResult_t res{};
+    int n = 0;
+    ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                               sizeof(wsb)) == HIPBLAS_STATUS_SUCCESS &&
+         hipblasLtMatmulAlgoGetHeuristic(*h, p.op, p.la, p.lb, p.lc, p.lc, pref, 1, &res, &n) ==
+             HIPBLAS_STATUS_SUCCESS &&
+         n > 0 && res.workspaceSize == 0;
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (ok) p.algo = res.algo;
+  }
+  p.ok = ok;
+  auto& slot = blt_plans[key] = p;
+  return ok ? &slot : nullptr;
+}
+}  // namespace
+
+// true when the call went to hipBLASLt (rc holds its status)
+static bool blt_gemm(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N, int64_t K, float* C,
+                     int64_t ldc, bool add, hipStream_t s, int* rc) {
+  hipblasLtHandle_t h = nullptr;
+  const BltPlan* p = blt_plan(M, N, K, lda, ldc, &h);
+  if (!p) return false;
+  const float alpha = 1.0f, beta = add ? 1.0f : 0.0f;
+  const hipblasStatus_t st = hipblasLtMatmul(h, p->op, &alpha, B, p->la, A, p->lb, &beta, C, p->lc, C, p->lc,
+                                             &p->algo, nullptr, 0, s);
+  *rc = st == HIPBLAS_STATUS_SUCCESS ? hip_status("qmoe_gemm(hipblaslt)")
+                                     : fail(QMOE_ERR_HIP, "qmoe_gemm: hipblasLtMatmul failed (%d)", int(st));
+  return true;
+}
+
 template <int MODE>
 static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M, int N, int K,
                        void* C, int64_t ldc, hipStream_t s) {
@@ -496,6 +581,10 @@ static int launch_tile(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
   using Small = pipe::Pipe<128, 128, 64, 2>;
   using Tiny = pipe::Pipe<64, 64, 64, 4>;
   auto count = [&](int bm, int bn) { return int64_t((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (MODE != QMOE_GEMM_STORE_BF16 && count(256, 256) >= 224 && K >= 2048) {
+    int rc = QMOE_OK;
+    if (blt_gemm(A, lda, B, M, N, K, static_cast<float*>(C), ldc, MODE == QMOE_GEMM_ADD_F32, s, &rc)) return rc;
+  }
   if (count(256, 256) >= 224 && N % 4 == 0 && ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0)
     return launch_wide<MODE>(A, lda, B, M, N, K, C, ldc, s);
   if (count(256, 256) >= 224) return launch_pipe<Big, 1, MODE>(A, lda, B, M, N, K, C, ldc, s);
