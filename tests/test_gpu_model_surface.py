@@ -4,10 +4,12 @@ prompts through ``generate`` (main.py:366, 480-486), the generate-mode driver
 (main.py:372-433, 634-649) and a local HF safetensors checkpoint loaded
 through ``NeuronQwen3MoeForCausalLM(path).load()`` (qwen_with_nki.py:8883-8997).
 
-Layer outputs are held to max-abs 2e-2 / mean relative 5e-3 of the oracle's
-fp32 layer on the rows whose expert choice matches the fp32 reference (rows
-near a router tie may legitimately choose differently; at most 10% of rows,
-and never one whose reference gap exceeds 1e-2).
+Layer outputs: the oracle routes from the product's own bf16 normed rows and
+the expert ids must match exactly wherever the k-th / (k+1)-th logit gap
+exceeds 1e-3; on every such row the output is held to max-abs 2e-2 / mean
+relative 5e-3 of the oracle's fp32 layer over those experts.  Against fp32
+routing, as a secondary check, every row with a 1e-2 gap and at least 90% of
+rows must agree.
 """
 
 import json
