@@ -540,37 +540,55 @@ def test_moe_block_prefill_zipf_T4096(dev, experts, router_w):
     assert_close_layer(got.cpu(), ref.cpu(), "moe block T=4096 Zipf(1.1)")
 
 
-def test_expert_seams_match_block(dev, experts, router_w):
-    """forward_selective_loading / torch_blockwise_matmul_inference seams give
-    the block's result for the same routing."""
-    announce("expert seams")
+@pytest.mark.parametrize("T", [8, 96])
+def test_expert_seams_match_block(dev, experts, router_w, T):
+    """forward_selective_loading (qwen_with_nki.py:3456-3478) and
+    torch_blockwise_matmul_inference (5872-5881, semantics 5728-5789) against
+    the oracle MoE over the same routing: the selective seam with the
+    L1-normalised softmax affinities of the chosen experts, the blockwise
+    seam with the masked affinities of the reference's block format (blocks
+    of 16 rows per expert, padding row id T).  The seams return the input
+    dtype, so they get fp32 rows (bf16 values) and return fp32.  T = 8 runs
+    the expert GEMVs (fp32 activations: 2e-3 / 1e-4), T = 96 the grouped MFMA
+    GEMMs (bf16 activations: 2e-2 / 5e-3).  Both also match the block's own
+    output at the layer bar."""
+    announce(f"expert seams T={T}")
     w13, w2 = experts
-    T = 96
-    g = torch.Generator(device=dev).manual_seed(42)
+    g = torch.Generator(device=dev).manual_seed(42 + T)
     x = bf16_randn((T, H), g, dev)
     blk = MoEBlock(router_w, w13, w2, K_TOP)
-    ref = blk(x)
+    ref_blk = blk(x)
     logits, tw, ti = blk.last_routing
     aff = torch.softmax(logits, dim=-1)
-    sel = blk.experts.forward_selective_loading(x, aff, ti)
-    # reference block format: per-expert blocks of B rows, padding row id T
+    xf = x.float()
+    sel = blk.experts.forward_selective_loading(xf, aff, ti)
     B = 16
     top = ti.long().cpu()
     blocks, b2e = [], []
     for e in range(E):
         toks = torch.nonzero((top == e).any(dim=1)).flatten().tolist()
-        for s in range(0, len(toks), B):
-            chunk = toks[s : s + B]
+        for s0 in range(0, len(toks), B):
+            chunk = toks[s0 : s0 + B]
             blocks.append(chunk + [T] * (B - len(chunk)))
             b2e.append(e)
     masked = torch.zeros(T, E, device=dev)
     masked.scatter_(1, ti.long(), tw)
     tpid = torch.tensor(blocks, dtype=torch.long, device=dev).flatten()
     bw = blk.experts.torch_blockwise_matmul_inference(
-        B, len(blocks), x, masked, tpid, torch.tensor(b2e, device=dev))
+        B, len(blocks), xf, masked, tpid, torch.tensor(b2e, device=dev))
     torch.cuda.synchronize()
-    assert_close_layer(sel.float().cpu(), ref.cpu(), "selective-loading seam", 2e-2, 1e-2)
-    assert_close_layer(bw.float().cpu(), ref.cpu(), "blockwise seam", 2e-2, 1e-2)
+    assert sel.dtype == torch.float32 and bw.dtype == torch.float32
+    chosen = torch.gather(aff.float().cpu(), 1, top)
+    w_sel = chosen / chosen.sum(dim=1, keepdim=True)
+    cache = _ExpertCache(w13, w2)
+    ref_sel = _oracle_rows(x.cpu(), top, w_sel, cache, range(T))
+    ref_bw = _oracle_rows(x.cpu(), top, tw.float().cpu(), cache, range(T))
+    tol = (2e-3, 1e-4) if T <= 48 else (2e-2, 5e-3)
+    assert_close_layer(sel.float().cpu(), ref_sel, "selective-loading seam vs oracle", *tol)
+    assert_close_layer(bw.float().cpu(), ref_bw, "blockwise seam vs oracle", *tol)
+    # the block runs other kernels (the decode block at T <= 8): the layer bar
+    assert_close_layer(sel.float().cpu(), ref_blk.cpu(), "selective-loading seam vs block", 2e-2, 5e-3)
+    assert_close_layer(bw.float().cpu(), ref_blk.cpu(), "blockwise seam vs block", 2e-2, 5e-3)
 
 
 # --------------------------------------------------------------------------- attention
