@@ -314,7 +314,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     import torch
 
     from qmoe import ops
-    from qmoe.moe import MoEBlock, TILE_M
+    from qmoe.moe import MoEBlock, tile_m_for
 
     g = torch.Generator(device=dev).manual_seed(77 + T)
     L = min(4, len(layers))
@@ -334,7 +334,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
     for l in range(L):
         _, tw, ti = ops.router_topk(xs[l], layers[l][0], K_TOP, biases[l])
         counts.append(torch.bincount(ti.long().flatten(), minlength=E))
-        routes.append(ops.moe_permute(ti, E, TILE_M))
+        routes.append(ops.moe_permute(ti, E, tile_m_for(T, K_TOP)))
         if l == 0 and zipf_s:
             hist = routing_histogram(ti, fits[0][1], T)
     cnt = torch.stack(counts).float().mean(0)
@@ -351,7 +351,7 @@ def bench_prefill(layers, dev, T=4096, reps=20, zipf_s=1.1):
         # T rows: only full 256 x 256 tiles, weights shared by T/256 tiles):
         # the expert kernels' rate when MFMA work is all there is.
         top = torch.arange(K_TOP, dtype=torch.int32, device=dev).repeat(T, 1)
-        droute = ops.moe_permute(top, E, TILE_M)
+        droute = ops.moe_permute(top, E, tile_m_for(T, K_TOP))
         dmean, _ = event_time_experts(
             lambda i: ops.moe_experts_grouped(xs[i % L], layers[i % L][1], layers[i % L][2], droute), 4 * L)
         dense = {"experts_us_mean": dmean * 1e3, "experts_TFLOPs": flops / (dmean * 1e-3) / 1e12}

@@ -26,8 +26,21 @@ from . import _lib, ops
 # 128 experts the two paths take the same time at T = 48 on MI355X: 242 us
 # per block, against 212 / 233 us at T = 32 and 270 / 248 us at T = 64.)
 GEMV_MAX_TOKENS = 48
-# Row tile of the prefill dispatch table: one 256 x 256 MFMA tile per (tile, panel).
+# Row tile of the prefill dispatch table: one (up to) 256 x 256 MFMA tile per
+# (tile, panel).
 TILE_M = _lib.GROUPED_MAX_TILE_M
+# Prompt sizes (up to this many routed (token, expert) pairs): 224-row tiles.
+# There the one launch is bound by the crowded experts' full tiles (a 256-row
+# gate_up item, then the tile's down items); 224 rows are 7 of the 8 32-row
+# MFMA blocks, for about two more tiles per layer (640-token prompt, deep
+# layers: 87.5 -> 82.8 and 88.2 -> 86.2 us, the same y_slot bits; 192 rows and
+# 1024 tokens or more were slower).
+SHORT_TILE_M, SHORT_TILE_MAX_PAIRS = 224, 6144
+
+
+def tile_m_for(T: int, k: int) -> int:
+    """Row tile of the dispatch table for T tokens routed to k experts each."""
+    return SHORT_TILE_M if T * k <= SHORT_TILE_MAX_PAIRS else TILE_M
 
 
 class ExpertMLPs:
@@ -52,7 +65,7 @@ class ExpertMLPs:
             residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Permute, run the experts, combine: ``residual + sum_j w_j * expert_j(x)`` (f32)."""
         T = x.shape[0]
-        route = ops.moe_permute(topk_idx, self.num_experts, TILE_M)
+        route = ops.moe_permute(topk_idx, self.num_experts, tile_m_for(T, topk_idx.shape[1]))
         if T <= GEMV_MAX_TOKENS:
             y = ops.moe_experts_gemv(x, self.w13, self.w2, route)
         else:
@@ -144,7 +157,7 @@ class MoEBlock:
             self.last_routing = (bufs.logits, bufs.topk_w, bufs.topk_idx)
             self.last_input = x
             return out
-        route = ops.moe_route(x, self.w_router, self.top_k, self.router_bias, TILE_M)
+        route = ops.moe_route(x, self.w_router, self.top_k, self.router_bias, tile_m_for(T, self.top_k))
         self.last_routing = (route.logits, route.topk_w, route.topk_idx)
         self.last_input = x
         if T <= GEMV_MAX_TOKENS:
