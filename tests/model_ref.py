@@ -47,6 +47,8 @@ class ReferenceModel:
         self.p, self.config, self.cfg = params, config, cfg_dict(config)
         self.kv = [None] * len(params["layers"])
         self.min_gap = float("inf")  # smallest k-th/(k+1)-th router logit gap seen
+        self.recording = False  # while set, _layer appends (input, output, router logits) to trace
+        self.trace = []
 
     def _layer(self, i, h, positions):
         lw = self.p["layers"][i]
@@ -74,7 +76,10 @@ class ReferenceModel:
         gap = top[:, k - 1] - top[:, k]
         self.min_gap = min(self.min_gap, float(gap.min()))
         self._gaps = gap if self._gaps is None else torch.minimum(self._gaps, gap)
-        return h1 + m.view(B, S, H)
+        out = h1 + m.view(B, S, H)
+        if self.recording:
+            self.trace.append((h.clone(), out.clone(), logits.clone()))
+        return out
 
     def logits(self, input_ids, positions):
         h = torch.nn.functional.embedding(input_ids, self.p["embed_tokens"]).float()
@@ -90,7 +95,9 @@ class ReferenceModel:
         B, S = prompt.shape
         dev = prompt.device
         pos = torch.arange(S, device=dev).expand(B, S)
+        self.recording, self.trace = True, []
         lg = self.logits(prompt, pos)
+        self.recording = False
         self.prompt_hidden, self.prompt_logits, self.prompt_gaps = self.last_hidden, lg, self.last_gaps
         toks, gaps = [lg.argmax(-1)], [_top2_gap(lg)]
         for t in range(1, n_new):
