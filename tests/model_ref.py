@@ -48,7 +48,8 @@ class ReferenceModel:
         self.kv = [None] * len(params["layers"])
         self.min_gap = float("inf")  # smallest k-th/(k+1)-th router logit gap seen
         self.recording = False  # while set, _layer appends (input, output, router logits) to trace
-        self.trace = []
+        self.trace = []  # per layer, the prompt pass of greedy()
+        self.step_trace = []  # per layer, greedy()'s first decode step
 
     def _layer(self, i, h, positions):
         lw = self.p["layers"][i]
@@ -102,7 +103,12 @@ class ReferenceModel:
         toks, gaps = [lg.argmax(-1)], [_top2_gap(lg)]
         for t in range(1, n_new):
             p = torch.full((B, 1), S + t - 1, device=dev)
-            lg = self.logits(toks[-1].view(B, 1), p)
+            if t == 1:  # record the first decode step apart from the prompt's trace
+                prompt_trace, self.trace, self.recording = self.trace, [], True
+                lg = self.logits(toks[-1].view(B, 1), p)
+                self.step_trace, self.trace, self.recording = self.trace, prompt_trace, False
+            else:
+                lg = self.logits(toks[-1].view(B, 1), p)
             toks.append(lg.argmax(-1))
             gaps.append(_top2_gap(lg))
         return torch.stack(toks, 1), gaps

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import announce, assert_close_layer, check_layer_moe, max_abs, mean_rel
+from gpu_util import announce, assert_close_layer, check_layer_moe, gap_mask, max_abs, mean_rel
 from model_ref import ReferenceModel, cfg_dict, layer_weights_f32
 
 import qwen_with_nki as qn
@@ -132,13 +132,14 @@ def test_model_greedy_matches_fp32_reference(dev, n_layers, prompt_len, n_new):
     # against the reference layer's output on every token whose 8 experts
     # are the reference's (at least 90% of tokens in every layer; the others
     # sit at a router near-tie, where the product routes from its bf16
-    # normed rows).  Layer 0 is held to mean relative 7e-3: its input is the
+    # normed rows).  Layer 0 is held to mean relative 1e-2: its input is the
     # token embedding (mean |h| 0.016 against 0.14-6 further on), so its
     # output is almost all attention + MoE update, and the bf16 storage of
     # the normed rows, of q/k/v (the bf16 KV cache) and of the attention
     # output alone puts the fp32 math 4.2e-3 from fp32 in layer 0's
-    # attention (1.7e-3 in layer 10); measured 5.9e-3 for the layer, every
-    # other layer 0.26-2.0e-3 (48 layers, 640 tokens).
+    # attention (1.7e-3 in layer 10); measured 5.9e-3 for the layer (7.0e-3
+    # at the decode step below), every other layer 0.26-2.2e-3 (48 layers,
+    # 640 tokens).
     k = cfg.num_experts_per_tok
     worst = (0.0, 1.0)
     for i, layer in enumerate(m.model.layers):
@@ -154,10 +155,46 @@ def test_model_greedy_matches_fp32_reference(dev, n_layers, prompt_len, n_new):
         got, want = h.cpu()[same], h_out.reshape(prompt_len, -1).cpu()[same]
         ma, mr = max_abs(got, want), mean_rel(got, want)
         worst = (max(worst[0], mr if i > 0 else 0.0), min(worst[1], frac))
-        bar = 7e-3 if i == 0 else 5e-3
+        bar = 1e-2 if i == 0 else 5e-3
         assert ma <= 2e-2 and mr <= bar, f"layer {i} teacher-forced: max abs {ma:.3e}, mean rel {mr:.3e}"
     print(f"  teacher-forced layers 1+: worst mean rel {worst[0]:.2e}, lowest expert agreement {worst[1]:.3f}",
           flush=True)
+    # The first decode step, teacher-forced the same way on the one-token path
+    # (GEMV QKV with the input norm, fused split attention over the prompt's
+    # cache rows the loop above wrote, o_proj GEMV, one-launch MoE block).
+    # Every layer: the oracle routes the product's own bf16 normed row and
+    # the expert ids must be the same wherever that gap exceeds 1e-3; where
+    # the product's experts are also the fp32 reference's (no near-tie
+    # between the bf16 and fp32 rows), the layer output meets the layer bar
+    # (layer 0: as above).
+    assert ref.step_trace and len(ref.step_trace) == n_layers
+    pos_d = torch.full((1,), prompt_len, device=dev, dtype=torch.int32)
+    checked, exact, worst_d, first_d = 0, 0, 0.0, float("nan")
+    for i, layer in enumerate(m.model.layers):
+        h_in, h_out, logits = ref.step_trace[i]
+        h = h_in.reshape(1, -1).contiguous().clone()
+        layer.run(h, pos_d, 1, 1, m.model.rope, prompt_len)
+        torch.cuda.synchronize()
+        idx = layer.mlp.last_routing[2].long().reshape(1, -1).cpu()
+        rl, _, ri = oracle.router_topk(layer.mlp.last_input.reshape(1, -1).cpu(), layer.mlp.w_router.cpu(), k)
+        if bool(gap_mask(rl, k)[0]):
+            assert torch.equal(idx, ri.long()), f"decode layer {i}: expert ids differ at a gap above 1e-3"
+            exact += 1
+        ours = torch.sort(idx, dim=1).values
+        theirs = torch.sort(torch.topk(logits.reshape(1, -1), k, dim=-1).indices.cpu(), dim=1).values
+        if not torch.equal(ours, theirs):
+            continue
+        ma, mr = max_abs(h.cpu(), h_out.reshape(1, -1).cpu()), mean_rel(h.cpu(), h_out.reshape(1, -1).cpu())
+        bar = 1e-2 if i == 0 else 5e-3
+        assert ma <= 2e-2 and mr <= bar, f"decode layer {i} teacher-forced: max abs {ma:.3e}, mean rel {mr:.3e}"
+        checked += 1
+        if i == 0:
+            first_d = mr
+        else:
+            worst_d = max(worst_d, mr)
+    print(f"  teacher-forced decode step: ids exact in {exact}/{n_layers} layers past the gap; {checked} layers "
+          f"on the fp32 experts, layer 0 mean rel {first_d:.2e}, worst of the others {worst_d:.2e}", flush=True)
+    assert checked >= (n_layers * 3) // 4
     if n_layers == 48:
         assert match == n_new  # the full workload: all 32 greedy tokens equal
     else:
