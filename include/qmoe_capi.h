@@ -10,6 +10,11 @@
  *   - All tensor arguments are caller-owned device pointers; outputs and
  *     workspaces are allocated by the caller.  No entry point allocates,
  *     frees or synchronises the host.
+ *   - An empty batch (T, rows, M, n or B * S of zero) is valid: the call
+ *     launches nothing and returns 0, and the buffers sized by that count
+ *     may be NULL.  Weights, caches and norm weights are still required.
+ *     qmoe_moe_permute / qmoe_moe_route still write the dispatch metadata
+ *     for zero pairs (all counts 0, no tiles).
  *   - bf16 values are passed as qmoe_bf16 (the raw 16-bit pattern).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream),
  *     so every call can be captured into a HIP graph.

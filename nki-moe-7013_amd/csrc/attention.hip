@@ -1242,8 +1242,8 @@ extern "C" int qmoe_qkv_norm_rope(const qmoe_bf16* x, const qmoe_bf16* wqkv,
                                   int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float eps,
                                   qmoe_bf16* q_out, qmoe_bf16* k_cache, qmoe_bf16* v_cache,
                                   float* workspace, qmoe_stream_t stream) {
-  QMOE_REQUIRE(x && wqkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && q_out &&
-                   k_cache && v_cache,
+  QMOE_REQUIRE(wqkv && q_norm_w && k_norm_w && rope_cos && rope_sin && k_cache && v_cache &&
+                   (B == 0 || S == 0 || (x && positions && q_out)),
                "qmoe_qkv_norm_rope: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_qkv_norm_rope: head_dim must be 128 (D=%lld)", (long long)D);
   QMOE_REQUIRE(H > 0 && H % 64 == 0, "qmoe_qkv_norm_rope: H %% 64 != 0");
@@ -1306,7 +1306,8 @@ extern "C" int qmoe_qkv_finish(const float* qkv, const qmoe_bf16* q_norm_w, cons
                                const int32_t* positions, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
                                int64_t D, int64_t S_max, float eps, qmoe_bf16* q_out, qmoe_bf16* k_cache,
                                qmoe_bf16* v_cache, qmoe_stream_t stream) {
-  QMOE_REQUIRE(qkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && q_out && k_cache && v_cache,
+  QMOE_REQUIRE(q_norm_w && k_norm_w && rope_cos && rope_sin && k_cache && v_cache &&
+                   (B == 0 || S == 0 || (qkv && positions && q_out)),
                "qmoe_qkv_finish: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_qkv_finish: head_dim must be 128 (D=%lld)", (long long)D);
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq + 2 * Hkv < 65536, "qmoe_qkv_finish: bad head counts");
@@ -1354,7 +1355,7 @@ static int ap_launch(const char* fn, const qmoe_bf16* q, const qmoe_bf16* k_cach
                      int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, int64_t start,
                      const int32_t* start_dev, float scale, void* ws, int64_t ws_bytes, qmoe_bf16* out,
                      qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && out, "%s: null pointer", fn);
+  QMOE_REQUIRE(k_cache && v_cache && (B == 0 || S == 0 || (q && out)), "%s: null pointer", fn);
   QMOE_REQUIRE(D == HD, "%s: head_dim must be 128", fn);
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq < 65536, "%s: bad heads", fn);
   QMOE_REQUIRE(B >= 0 && B < 65536 && S >= 0 && S <= S_max && start >= 0 && start + S <= S_max,
@@ -1407,7 +1408,7 @@ extern "C" int qmoe_attn_prefill_ws(const qmoe_bf16* q, const qmoe_bf16* k_cache
 extern "C" int qmoe_attn_prefill_at(const qmoe_bf16* q, const qmoe_bf16* k_cache, const qmoe_bf16* v_cache,
                                     int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max,
                                     const int32_t* start, float scale, qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(start, "qmoe_attn_prefill_at: null pointer");
+  QMOE_REQUIRE(start || B == 0 || S == 0, "qmoe_attn_prefill_at: null pointer");
   return qmoe::ap_launch("qmoe_attn_prefill_at", q, k_cache, v_cache, B, S, Hq, Hkv, D, S_max, 0, start, scale,
                          nullptr, 0, out, stream);
 }
@@ -1471,7 +1472,7 @@ extern "C" int qmoe_attn_decode(const qmoe_bf16* q, const qmoe_bf16* k_cache,
                                 const qmoe_bf16* v_cache, const int32_t* ctx_len, int64_t B,
                                 int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, float scale,
                                 float* partial, qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && ctx_len && partial && out, "qmoe_attn_decode: null pointer");
+  QMOE_REQUIRE(k_cache && v_cache && (B == 0 || (q && ctx_len && partial && out)), "qmoe_attn_decode: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_attn_decode: head_dim must be 128");
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536,
                "qmoe_attn_decode: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
@@ -1484,7 +1485,8 @@ extern "C" int qmoe_attn_decode_bucket(const qmoe_bf16* q, const qmoe_bf16* k_ca
                                        const qmoe_bf16* v_cache, const int32_t* ctx_len, int64_t B,
                                        int64_t Hq, int64_t Hkv, int64_t D, int64_t S_max, int64_t max_ctx,
                                        float scale, float* partial, qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && ctx_len && partial && out, "qmoe_attn_decode_bucket: null pointer");
+  QMOE_REQUIRE(k_cache && v_cache && (B == 0 || (q && ctx_len && partial && out)),
+               "qmoe_attn_decode_bucket: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_attn_decode_bucket: head_dim must be 128");
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536,
                "qmoe_attn_decode_bucket: need Hq %% Hkv == 0 and Hq / Hkv <= 16");
@@ -1499,8 +1501,8 @@ extern "C" int qmoe_attn_decode_fused(const float* qkv, const qmoe_bf16* q_norm_
                                       const int32_t* positions, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                       int64_t S_max, int64_t max_ctx, float eps, float scale, qmoe_bf16* k_cache,
                                       qmoe_bf16* v_cache, float* partial, qmoe_bf16* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(qkv && q_norm_w && k_norm_w && rope_cos && rope_sin && positions && k_cache && v_cache && partial &&
-                   out,
+  QMOE_REQUIRE(q_norm_w && k_norm_w && rope_cos && rope_sin && k_cache && v_cache &&
+                   (B == 0 || (qkv && positions && partial && out)),
                "qmoe_attn_decode_fused: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_attn_decode_fused: head_dim must be 128");
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536 && Hq + 2 * Hkv < 65536,
@@ -1518,7 +1520,7 @@ extern "C" int qmoe_attn_decode_chunk(const qmoe_bf16* q, const qmoe_bf16* k_cac
                                       const int32_t* start, int64_t B, int64_t S, int64_t Hq, int64_t Hkv,
                                       int64_t D, int64_t S_max, float scale, float* partial, qmoe_bf16* out,
                                       qmoe_stream_t stream) {
-  QMOE_REQUIRE(q && k_cache && v_cache && start && partial && out, "qmoe_attn_decode_chunk: null pointer");
+  QMOE_REQUIRE(k_cache && v_cache && (B == 0 || (q && start && partial && out)), "qmoe_attn_decode_chunk: null pointer");
   QMOE_REQUIRE(D == HD, "qmoe_attn_decode_chunk: head_dim must be 128");
   QMOE_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= AD_MAX_G && Hkv < 65536,
                "qmoe_attn_decode_chunk: need Hq %% Hkv == 0 and Hq / Hkv <= 16");

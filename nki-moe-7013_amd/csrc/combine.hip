@@ -141,7 +141,7 @@ extern "C" int qmoe_moe_combine(const void* y_slot, int y_is_bf16, const int32_t
                                 const float* topk_w, const float* residual, int64_t T, int64_t k,
                                 int64_t H, float* out, qmoe_stream_t stream) {
   using namespace qmoe;
-  QMOE_REQUIRE(y_slot && token_slot && topk_w && out, "qmoe_moe_combine: null pointer");
+  QMOE_REQUIRE(T == 0 || (y_slot && token_slot && topk_w && out), "qmoe_moe_combine: null pointer");
   QMOE_REQUIRE(T >= 0 && T < (1 << 30) && k > 0 && k <= 64, "qmoe_moe_combine: bad T/k");
   QMOE_REQUIRE(H > 0 && H % 4 == 0 && H < (1 << 24), "qmoe_moe_combine: H %% 4 != 0");
   if (T == 0) return QMOE_OK;
@@ -163,7 +163,8 @@ extern "C" int qmoe_moe_combine_norm(const void* y_slot, int y_is_bf16, const in
                                      int64_t H, float* out, const qmoe_bf16* rms_w, float eps, qmoe_bf16* x_out,
                                      qmoe_stream_t stream) {
   using namespace qmoe;
-  QMOE_REQUIRE(y_slot && token_slot && topk_w && out && rms_w && x_out, "qmoe_moe_combine_norm: null pointer");
+  QMOE_REQUIRE(rms_w && (T == 0 || (y_slot && token_slot && topk_w && out && x_out)),
+               "qmoe_moe_combine_norm: null pointer");
   QMOE_REQUIRE(T >= 0 && T < (1 << 30) && k > 0 && k <= 64, "qmoe_moe_combine_norm: bad T/k");
   QMOE_REQUIRE(H > 0 && H % 4 == 0 && H <= NORM_THREADS * 4 * NORM_MAX_CHUNKS,
                "qmoe_moe_combine_norm: H must be a multiple of 4 and <= 8192 (H=%lld)", (long long)H);

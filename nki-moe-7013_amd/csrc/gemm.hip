@@ -946,13 +946,14 @@ static int launch_gemv(const uint16_t* A, int64_t lda, const uint16_t* B, int M,
 
 int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t M, int64_t N,
                 int64_t K, int mode, void* C, int64_t ldc, hipStream_t s) {
-  QMOE_REQUIRE(A && B && C, "qmoe_gemm: null pointer");
-  QMOE_REQUIRE(M > 0 && N > 0 && K > 0, "qmoe_gemm: empty shape M=%lld N=%lld K=%lld",
+  QMOE_REQUIRE(B && (M == 0 || (A && C)), "qmoe_gemm: null pointer");
+  QMOE_REQUIRE(M >= 0 && N > 0 && K > 0, "qmoe_gemm: empty shape M=%lld N=%lld K=%lld",
                (long long)M, (long long)N, (long long)K);
   QMOE_REQUIRE(mode >= 0 && mode <= 2, "qmoe_gemm: bad mode %d", mode);
   QMOE_REQUIRE(lda >= K && ldc >= N, "qmoe_gemm: lda/ldc smaller than the row length");
   QMOE_REQUIRE(lda % 8 == 0, "qmoe_gemm: lda must be a multiple of 8");
   QMOE_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31), "qmoe_gemm: dims overflow");
+  if (M == 0) return QMOE_OK;
   if (M <= 16 && M * K <= 32768) {
     QMOE_REQUIRE(K % 512 == 0, "qmoe_gemm: gemv path needs K %% 512 == 0 (K=%lld)", (long long)K);
     switch (mode) {
@@ -1073,7 +1074,7 @@ extern "C" int qmoe_gemm_ws_add_rmsnorm(const qmoe_bf16* A, int64_t lda, const q
                                        int64_t K, float* C, const qmoe_bf16* rms_w, float eps, qmoe_bf16* x_out,
                                        void* workspace, int64_t workspace_bytes, qmoe_stream_t stream) {
   using namespace qmoe;
-  QMOE_REQUIRE(A && B && C && rms_w && x_out, "qmoe_gemm_ws_add_rmsnorm: null pointer");
+  QMOE_REQUIRE(B && rms_w && (M == 0 || (A && C && x_out)), "qmoe_gemm_ws_add_rmsnorm: null pointer");
   QMOE_REQUIRE(M >= 0 && M < (1ll << 31) && N > 0 && K > 0, "qmoe_gemm_ws_add_rmsnorm: bad shape");
   QMOE_REQUIRE(N % 4 == 0 && N <= NORM_THREADS * 4 * NORM_MAX_CHUNKS,
                "qmoe_gemm_ws_add_rmsnorm: N must be a multiple of 4 and <= 8192 (N=%lld)", (long long)N);

@@ -105,7 +105,7 @@ extern "C" int64_t qmoe_argmax_workspace(int64_t rows) {
 
 extern "C" int qmoe_argmax(const float* x, int64_t rows, int64_t n, int64_t ldx, void* workspace,
                            int64_t workspace_bytes, int64_t* out, qmoe_stream_t stream) {
-  QMOE_REQUIRE(x && workspace && out, "qmoe_argmax: null pointer");
+  QMOE_REQUIRE(rows == 0 || (x && workspace && out), "qmoe_argmax: null pointer");
   QMOE_REQUIRE(rows >= 0 && rows < 65536 && n > 0 && n < (1ll << 31) && ldx >= n,
                "qmoe_argmax: bad rows/n/ldx");
   QMOE_REQUIRE(workspace_bytes >= qmoe_argmax_workspace(rows), "qmoe_argmax: workspace too small");
@@ -121,7 +121,7 @@ extern "C" int qmoe_argmax(const float* x, int64_t rows, int64_t n, int64_t ldx,
 
 extern "C" int qmoe_embed(const qmoe_bf16* table, int64_t V, int64_t H, const int64_t* ids, int64_t n,
                           float* out, int32_t* err, qmoe_stream_t stream) {
-  QMOE_REQUIRE(table && ids && out && err, "qmoe_embed: null pointer");
+  QMOE_REQUIRE(table && err && (n == 0 || (ids && out)), "qmoe_embed: null pointer");
   QMOE_REQUIRE(V > 0 && H > 0 && H % 4 == 0 && H < (1 << 24), "qmoe_embed: bad V/H (H %% 4 == 0)");
   QMOE_REQUIRE(n >= 0 && n < (1ll << 31), "qmoe_embed: bad n");
   if (n == 0) return QMOE_OK;

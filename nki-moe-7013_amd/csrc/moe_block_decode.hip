@@ -795,9 +795,9 @@ static int check_block_args(const char* fn, const qmoe_bf16* x, const float* h,
                             int64_t I, int64_t E, int64_t k, const float* logits,
                             const int32_t* topk_idx, const float* topk_w, const qmoe_bf16* x_out,
                             const float* out) {
-  QMOE_REQUIRE(w_router && w13 && w2 && logits && topk_idx && topk_w && out, "%s: null pointer", fn);
-  QMOE_REQUIRE((x != nullptr) != (h != nullptr), "%s: pass exactly one of x and h", fn);
-  QMOE_REQUIRE(!h || (rms_w && x_out), "%s: h needs rms_w and x_out", fn);
+  QMOE_REQUIRE(w_router && w13 && w2 && (T == 0 || (logits && topk_idx && topk_w && out)), "%s: null pointer", fn);
+  QMOE_REQUIRE(T == 0 || (x != nullptr) != (h != nullptr), "%s: pass exactly one of x and h", fn);
+  QMOE_REQUIRE(!h || (rms_w && (T == 0 || x_out)), "%s: h needs rms_w and x_out", fn);
   QMOE_REQUIRE(T >= 0 && T <= BLK_MAX_T, "%s: T must be <= 8 (T=%lld)", fn, (long long)T);
   QMOE_REQUIRE(E > 0 && E <= ROUTER_MAX_E && k > 0 && k <= ROUTER_MAX_K && k <= E && T * k <= BLK_MAX_PAIRS,
                "%s: need E <= 256, k <= min(16, E), T*k <= 64", fn);

@@ -236,7 +236,7 @@ extern "C" int qmoe_moe_experts_gemv(const qmoe_bf16* x, const qmoe_bf16* w13,
                                      const int32_t* meta, int64_t T, int64_t H, int64_t I,
                                      int64_t E, int64_t k, float* act, float* y_slot,
                                      qmoe_stream_t stream) {
-  QMOE_REQUIRE(x && w13 && w2 && offsets && slot_token && active && meta && act && y_slot,
+  QMOE_REQUIRE(w13 && w2 && offsets && active && meta && (T == 0 || (x && slot_token && act && y_slot)),
                "qmoe_moe_experts_gemv: null pointer");
   int rc = check_dec_shapes("qmoe_moe_experts_gemv", T, H, I, E, k);
   if (rc) return rc;

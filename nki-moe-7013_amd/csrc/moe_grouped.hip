@@ -422,7 +422,7 @@ extern "C" int qmoe_moe_experts_grouped(const qmoe_bf16* x, const qmoe_bf16* w13
                                         int64_t E, int64_t k, qmoe_bf16* act, qmoe_bf16* y_slot,
                                         qmoe_stream_t stream) {
   using namespace qmoe;
-  QMOE_REQUIRE(x && w13 && w2 && slot_token && tiles && meta && act && y_slot,
+  QMOE_REQUIRE(w13 && w2 && tiles && meta && (T == 0 || (x && slot_token && act && y_slot)),
                "qmoe_moe_experts_grouped: null pointer");
   QMOE_REQUIRE(T >= 0 && T * k < (1ll << 30), "qmoe_moe_experts_grouped: bad T");
   QMOE_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= E, "qmoe_moe_experts_grouped: bad E/k");

@@ -48,7 +48,7 @@ extern "C" int qmoe_rmsnorm_residual(const float* x, const float* delta, const q
                                      int64_t rows, int64_t H, float eps, float* h_out,
                                      qmoe_bf16* y_out, qmoe_stream_t stream) {
   using namespace qmoe;
-  QMOE_REQUIRE(x && w && y_out, "qmoe_rmsnorm_residual: null pointer");
+  QMOE_REQUIRE(w && (rows == 0 || (x && y_out)), "qmoe_rmsnorm_residual: null pointer");
   QMOE_REQUIRE(rows >= 0 && rows < (1ll << 31), "qmoe_rmsnorm_residual: bad rows %lld", (long long)rows);
   QMOE_REQUIRE(H > 0 && H % 4 == 0 && H <= NORM_THREADS * 4 * NORM_MAX_CHUNKS,
                "qmoe_rmsnorm_residual: H must be a multiple of 4 and <= 8192 (H=%lld)", (long long)H);

@@ -156,7 +156,7 @@ int permute_launch(const int32_t* topk_idx, int64_t T, int64_t k, int64_t E, int
                    int64_t max_tiles, int32_t* counts, int32_t* offsets, int32_t* slot_token,
                    int32_t* token_slot, int32_t* active, int32_t* tiles, int32_t* meta,
                    hipStream_t s) {
-  QMOE_REQUIRE(topk_idx && counts && offsets && slot_token && token_slot && active && tiles && meta,
+  QMOE_REQUIRE(counts && offsets && active && tiles && meta && (T == 0 || (topk_idx && slot_token && token_slot)),
                "qmoe_moe_permute: null pointer");
   QMOE_REQUIRE(E > 0 && E <= PERM_MAX_E, "qmoe_moe_permute: E must be in [1, 256]");
   QMOE_REQUIRE(k > 0 && k <= E, "qmoe_moe_permute: k must be in [1, E]");

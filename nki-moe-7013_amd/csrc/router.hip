@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(float* __restrict__ l
 int router_launch(const uint16_t* x, const uint16_t* w_router, const float* bias, int64_t T,
                   int64_t H, int64_t E, int64_t k, int32_t* topk_idx, float* topk_w, float* logits,
                   void* workspace, int64_t workspace_bytes, hipStream_t s) {
-  QMOE_REQUIRE(x && w_router && topk_idx && topk_w && logits,
+  QMOE_REQUIRE(w_router && (T == 0 || (x && topk_idx && topk_w && logits)),
                "qmoe_router_topk: null pointer (logits is required)");
   QMOE_REQUIRE(T >= 0 && T < (1ll << 31), "qmoe_router_topk: bad T");
   QMOE_REQUIRE(E > 0 && E <= ROUTER_MAX_E, "qmoe_router_topk: E must be in [1, 256] (E=%lld)", (long long)E);

@@ -133,6 +133,51 @@ def test_invalid_arguments_rejected_before_launch(call, msg):
     assert msg in _lib.last_error()
 
 
+@pytest.mark.parametrize(
+    "call",
+    [
+        # rows = 0: x, delta, h_out and y_out NULL; the norm weight still given
+        lambda l: l.qmoe_rmsnorm_residual(None, None, 1, 0, 2048, 1e-6, None, None, None),
+        lambda l: l.qmoe_router_topk(None, 1, None, 0, 2048, 128, 8, None, None, None, None),
+        lambda l: l.qmoe_moe_combine(None, 1, None, None, None, 0, 8, 2048, None, None),
+        lambda l: l.qmoe_moe_combine_norm(None, 1, None, None, None, 0, 8, 2048, None, 1, 1e-6, None, None),
+        lambda l: l.qmoe_moe_experts_grouped(None, 1, 1, None, 1, 1, 128, 0, 2048, 768, 128, 8, None, None, None),
+        lambda l: l.qmoe_moe_experts_gemv(None, 1, 1, 1, None, 1, 1, 0, 2048, 768, 128, 8, None, None, None),
+        lambda l: l.qmoe_gemm(None, 2048, 1, 0, 128, 2048, 0, None, 128, None),
+        lambda l: l.qmoe_gemm_ws_add_rmsnorm(None, 4096, 1, 0, 2048, 4096, None, 1, 1e-6, None, None, 0, None),
+        lambda l: l.qmoe_qkv_norm_rope(None, 1, 1, 1, 1, 1, 10, None, 0, 1, 2048, 32, 4, 128, 10, 1e-6,
+                                       None, 1, 1, None, None),
+        lambda l: l.qmoe_attn_prefill(None, 1, 1, 0, 10, 32, 4, 128, 16, 0, 0.1, None, None),
+        lambda l: l.qmoe_attn_prefill_at(None, 1, 1, 0, 10, 32, 4, 128, 16, None, 0.1, None, None),
+        lambda l: l.qmoe_attn_decode(None, 1, 1, None, 0, 32, 4, 128, 16, 0.1, None, None, None),
+        lambda l: l.qmoe_argmax(None, 0, 100, 100, None, 0, None, None),
+        lambda l: l.qmoe_embed(1, 100, 8, None, 0, None, 1, None),
+        lambda l: l.qmoe_moe_decode_block(None, None, None, 1e-6, 1, None, 1, 1, None, 0, 2048, 768, 128, 8,
+                                          None, None, None, 1, 1 << 20, None, None, None),
+    ],
+)
+def test_empty_batch_accepts_null_row_buffers(call):
+    """A zero-row call launches nothing and returns 0, and the buffers sized
+    by the row count may be NULL (torch hands an empty tensor over as
+    address 0).  These calls return before any HIP call."""
+    if torch.cuda.is_available():
+        pytest.skip("host-side validation test; runs only where no GPU is visible")
+    rc = call(_lib.lib())
+    assert rc == _lib.QMOE_OK, _lib.last_error()
+
+
+def test_empty_batch_still_requires_weights():
+    """Weights are not sized by the batch: NULL stays an error at T = 0."""
+    if torch.cuda.is_available():
+        pytest.skip("host-side validation test; runs only where no GPU is visible")
+    l = _lib.lib()
+    assert l.qmoe_rmsnorm_residual(None, None, None, 0, 2048, 1e-6, None, None, None) == _lib.QMOE_ERR_INVALID
+    assert "null pointer" in _lib.last_error()
+    assert l.qmoe_moe_experts_grouped(None, None, 1, None, 1, 1, 128, 0, 2048, 768, 128, 8, None, None,
+                                      None) == _lib.QMOE_ERR_INVALID
+    assert l.qmoe_gemm(None, 2048, None, 0, 128, 2048, 0, None, 128, None) == _lib.QMOE_ERR_INVALID
+
+
 def test_python_wrappers_reject_host_tensors():
     a = torch.zeros(4, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU"):

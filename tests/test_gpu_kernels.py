@@ -1255,3 +1255,43 @@ def test_argmax_graph_replays(dev):
         graph.replay()
         torch.cuda.synchronize()
         assert int(out.item()) == (i * 7919) % n == int(x.cpu().argmax())
+
+
+# --------------------------------------------------------------------------- empty batch
+def test_empty_batch_through_every_op(dev, experts, router_w):
+    """T = 0 is a valid batch: every op returns empty outputs and launches
+    nothing, and the dispatch metadata says zero pairs (all counts 0, no
+    tiles, no active experts, no error).  Torch hands the empty tensors over
+    as address 0, which the library accepts for buffers of zero elements."""
+    announce("empty batch T=0")
+    w13, w2 = experts
+    x0 = torch.empty(0, H, dtype=torch.bfloat16, device=dev)
+    h0 = torch.empty(0, H, device=dev)
+    nw = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    ti0 = torch.empty(0, K_TOP, dtype=torch.int32, device=dev)
+    tw0 = torch.empty(0, K_TOP, device=dev)
+
+    y = ops.rmsnorm_residual(h0, nw, 1e-6)
+    assert y.shape == (0, H)
+    logits, w, idx = ops.router_topk(x0, router_w, K_TOP)
+    assert idx.shape == (0, K_TOP) and w.shape == (0, K_TOP) and logits.shape == (0, E)
+    for tile_m in (128, 256):
+        route = ops.moe_permute(ti0, E, tile_m)
+        torch.cuda.synchronize()
+        meta = route.meta.cpu()
+        assert route.counts.cpu().eq(0).all() and route.offsets.cpu().eq(0).all()
+        assert meta[:3].tolist() == [0, 0, 0]
+        y_slot = ops.moe_experts_grouped(x0, w13, w2, route)
+        assert y_slot.shape == (0, H)
+        out = ops.moe_combine(y_slot, route, tw0)
+        assert out.shape == (0, H)
+        out, xn = ops.moe_combine(y_slot, route, tw0, residual=h0, out=h0, norm=(nw, 1e-6))
+        assert out.shape == (0, H) and xn.shape == (0, H)
+    route = ops.moe_route(x0, router_w, K_TOP, None, 256)
+    torch.cuda.synchronize()
+    assert route.meta.cpu()[:3].tolist() == [0, 0, 0]
+    assert ops.moe_experts_gemv(x0, w13, w2, ops.moe_permute(ti0, E, 128)).shape == (0, H)
+    assert ops.gemm(x0, router_w).shape == (0, E)
+    assert ops.moe_decode_block(router_w, w13, w2, K_TOP, x=x0).shape == (0, H)
+    assert MoEBlock(router_w, w13, w2, K_TOP)(x0).shape == (0, H)
+    torch.cuda.synchronize()
