@@ -14,6 +14,7 @@ Host-side mirror of the reference's MoE module surface:
 
 from __future__ import annotations
 
+import dataclasses
 from types import SimpleNamespace
 from typing import Optional
 
@@ -55,10 +56,10 @@ class ExpertMLPs:
         self.intermediate_size = w13.shape[1] // 2
         self.top_k = top_k
         self.normalize_top_k_affinities = normalize_top_k_affinities
-        # NxDI's RoutedExpertsMLPOpsConfig flag the prefill seam reads
-        # (qwen_with_nki.py:5768): scale the input rows by the affinity before
-        # the MLP instead of the output after it.  Only the default (False,
-        # Qwen3's setting) is implemented; the seam rejects True.
+        # NxDI's RoutedExpertsMLPOpsConfig flag the seams read
+        # (qwen_with_nki.py:5768, 3449): True scales each pair's input row by
+        # its affinity before the MLP instead of the output after it (Qwen3
+        # leaves it False).
         self.routed_experts_mlp_config = SimpleNamespace(early_expert_affinity_modulation=False)
 
     def run(self, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor,
@@ -72,6 +73,28 @@ class ExpertMLPs:
             y = ops.moe_experts_grouped(x, self.w13, self.w2, route)
         return ops.moe_combine(y, route, topk_w, residual, out)
 
+    def run_early(self, x: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor) -> torch.Tensor:
+        """``sum_j expert_j(w_j * x)`` (f32): early affinity modulation, the
+        ``early_expert_affinity_modulation`` branch of qwen_with_nki.py:5768-5775.
+
+        Every (token, expert) pair p = t*k + j becomes its own input row
+        ``bf16(w_tj * x_t)`` (the experts read bf16) routed to its one expert;
+        the combine kernel then sums each token's k outputs with unit weights
+        in the fixed order j = 0..k-1, through the pair dispatch's own slot map."""
+        T, k = topk_idx.shape
+        if T == 0:
+            return torch.zeros(0, x.shape[1], dtype=torch.float32, device=x.device)
+        rows = (x.float().repeat_interleave(k, dim=0) * topk_w.reshape(T * k, 1).float()).to(torch.bfloat16)
+        pair_idx = topk_idx.reshape(T * k, 1).contiguous()
+        route = ops.moe_permute(pair_idx, self.num_experts, tile_m_for(T * k, 1))
+        if T * k <= GEMV_MAX_TOKENS:
+            y = ops.moe_experts_gemv(rows, self.w13, self.w2, route)
+        else:
+            y = ops.moe_experts_grouped(rows, self.w13, self.w2, route)
+        # token_slot of the pair dispatch, read as [T, k]: entry (t, j) is the slot of pair t*k + j
+        per_token = dataclasses.replace(route, T=T, k=k)
+        return ops.moe_combine(y, per_token, torch.ones(T, k, dtype=torch.float32, device=x.device))
+
     # -- reference seams -------------------------------------------------------
     def forward_selective_loading(self, hidden_states: torch.Tensor, expert_affinities: torch.Tensor,
                                   expert_index: torch.Tensor) -> torch.Tensor:
@@ -79,16 +102,19 @@ class ExpertMLPs:
         affinities from ``expert_affinities[T,E]``, L1-normalise them when
         ``normalize_top_k_affinities``, and return ``sum_j aff_j * mlp_j(x)``
         as ``[T,H]`` in the input dtype."""
-        if getattr(self.routed_experts_mlp_config, "early_expert_affinity_modulation", False):
-            raise ValueError("early_expert_affinity_modulation=True is not implemented (the reference "
-                             "routes it to the stock path, qwen_with_nki.py:3449)")
         T = hidden_states.shape[0]
         idx = expert_index.to(torch.int32).contiguous()
         chosen = torch.gather(expert_affinities.float(), 1, expert_index.long())
         if self.normalize_top_k_affinities:
             chosen = torch.nn.functional.normalize(chosen, p=1.0, dim=1)
-        out = self.run(hidden_states.to(torch.bfloat16).contiguous(), idx, chosen.contiguous())
+        x = hidden_states.to(torch.bfloat16).contiguous()
+        if self._early():
+            return self.run_early(x, idx, chosen.contiguous()).to(hidden_states.dtype).view(T, -1)
+        out = self.run(x, idx, chosen.contiguous())
         return out.to(hidden_states.dtype).view(T, -1)
+
+    def _early(self) -> bool:
+        return bool(getattr(self.routed_experts_mlp_config, "early_expert_affinity_modulation", False))
 
     def torch_blockwise_matmul_inference(self, block_size, num_blocks, hidden_states,
                                          expert_affinities_masked, token_position_to_id,
@@ -102,10 +128,6 @@ class ExpertMLPs:
         through the build's own permutation (a token never repeats within
         one expert, so the reference's duplicate redirection is not needed).
         """
-        if getattr(self.routed_experts_mlp_config, "early_expert_affinity_modulation", False):
-            raise ValueError("early_expert_affinity_modulation=True (affinity applied to the MLP input, "
-                             "qwen_with_nki.py:5768-5775) is not implemented: the experts here scale "
-                             "the MLP output by the affinity")
         T, H = hidden_states.shape
         E = self.num_experts
         tok = token_position_to_id.view(int(num_blocks), int(block_size)).long()
@@ -122,8 +144,9 @@ class ExpertMLPs:
         top_w, top_i = torch.topk(aff, k, dim=1)
         if not bool((top_w >= 0).all()):
             raise ValueError("every token must be routed to the same number of experts")
-        out = self.run(hidden_states.to(torch.bfloat16).contiguous(), top_i.to(torch.int32).contiguous(),
-                       top_w.contiguous())
+        run = self.run_early if self._early() else self.run
+        out = run(hidden_states.to(torch.bfloat16).contiguous(), top_i.to(torch.int32).contiguous(),
+                  top_w.contiguous())
         return out.to(hidden_states.dtype)
 
 

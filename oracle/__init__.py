@@ -20,6 +20,7 @@ from .qwen3_moe import (  # noqa: F401
     expert_swiglu,
     moe_block_prefill,
     moe_block_decode,
+    moe_experts_early,
     moe_block,
     rope_tables,
     apply_rope,

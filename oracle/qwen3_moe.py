@@ -50,6 +50,12 @@ PINNING: Dict[str, str] = {
         "brute force; k=1 with a single expert reduces to a dense SwiGLU MLP"
     ),
     "moe_block_decode": "equals moe_block_prefill and the float64 brute force",
+    "moe_experts_early": (
+        "k=1 (affinity 1) reduces to moe_block_prefill's output; the small-"
+        "affinity limit silu(z) ~ z/2 fixes out/a^2 -> 0.5 ((x Wg)*(x Wu)) Wd in "
+        "closed form (an affinity applied to the output would scale as a); "
+        "the result is the sum of separate one-pair calls"
+    ),
     "apply_rope": (
         "transformers apply_rotary_pos_emb / Qwen3MoeRotaryEmbedding golden "
         "fixtures; position 0 is the identity; per-pair norm preservation; "
@@ -231,6 +237,27 @@ def moe_block_decode(
         )
         outs.append(torch.sum(per_e * top_w[t].unsqueeze(1), dim=0))
     return torch.stack(outs), top_i, top_w, logits
+
+
+def moe_experts_early(x: torch.Tensor, top_i: torch.Tensor, top_w: torch.Tensor, experts) -> torch.Tensor:
+    """Routed experts with early affinity modulation: each selected (token,
+    expert) pair's input row is multiplied by its affinity before the MLP,
+    and the MLP outputs are added unscaled -- the
+    ``early_expert_affinity_modulation`` branch of the blockwise loop
+    (qwen_with_nki.py:5768-5775): per expert, gather its rows,
+    ``x[tok] * aff[tok, e]`` -> ``mlp_op`` -> ``output[tok] += ...``.
+
+    ``top_i``/``top_w`` ``[T,k]``; ``experts[e]`` gives ``(gate_up (H, 2I),
+    down (I, H))``.  Returns ``out[T,H]`` in fp32.
+    """
+    T, H = x.shape
+    out = torch.zeros(T, H, dtype=torch.float32)
+    xf = x.float()
+    for e in torch.unique(top_i).tolist():
+        tok, j = torch.nonzero(top_i == e, as_tuple=True)
+        rows = xf[tok] * top_w[tok, j].float().unsqueeze(1)
+        out.index_add_(0, tok, expert_swiglu(rows, *experts[int(e)]))
+    return out
 
 
 def moe_block(x, w_router, gate_up, down, k, bias=None):

@@ -540,6 +540,25 @@ def test_moe_block_prefill_zipf_T4096(dev, experts, router_w):
     assert_close_layer(got.cpu(), ref.cpu(), "moe block T=4096 Zipf(1.1)")
 
 
+def _blockwise_seam(ex, xf, ti, tw, B=16):
+    """Call torch_blockwise_matmul_inference with the reference's block
+    format for routing (ti, tw): blocks of B token rows per expert, padding
+    rows pointing at the extra row T, affinities masked to the chosen experts."""
+    T, dev = xf.shape[0], xf.device
+    top = ti.long().cpu()
+    blocks, b2e = [], []
+    for e in range(E):
+        toks = torch.nonzero((top == e).any(dim=1)).flatten().tolist()
+        for s0 in range(0, len(toks), B):
+            chunk = toks[s0 : s0 + B]
+            blocks.append(chunk + [T] * (B - len(chunk)))
+            b2e.append(e)
+    masked = torch.zeros(T, E, device=dev)
+    masked.scatter_(1, ti.long(), tw)
+    tpid = torch.tensor(blocks, dtype=torch.long, device=dev).flatten()
+    return ex.torch_blockwise_matmul_inference(B, len(blocks), xf, masked, tpid, torch.tensor(b2e, device=dev))
+
+
 @pytest.mark.parametrize("T", [8, 96])
 def test_expert_seams_match_block(dev, experts, router_w, T):
     """forward_selective_loading (qwen_with_nki.py:3456-3478) and
@@ -562,20 +581,8 @@ def test_expert_seams_match_block(dev, experts, router_w, T):
     aff = torch.softmax(logits, dim=-1)
     xf = x.float()
     sel = blk.experts.forward_selective_loading(xf, aff, ti)
-    B = 16
     top = ti.long().cpu()
-    blocks, b2e = [], []
-    for e in range(E):
-        toks = torch.nonzero((top == e).any(dim=1)).flatten().tolist()
-        for s0 in range(0, len(toks), B):
-            chunk = toks[s0 : s0 + B]
-            blocks.append(chunk + [T] * (B - len(chunk)))
-            b2e.append(e)
-    masked = torch.zeros(T, E, device=dev)
-    masked.scatter_(1, ti.long(), tw)
-    tpid = torch.tensor(blocks, dtype=torch.long, device=dev).flatten()
-    bw = blk.experts.torch_blockwise_matmul_inference(
-        B, len(blocks), xf, masked, tpid, torch.tensor(b2e, device=dev))
+    bw = _blockwise_seam(blk.experts, xf, ti, tw)
     torch.cuda.synchronize()
     assert sel.dtype == torch.float32 and bw.dtype == torch.float32
     chosen = torch.gather(aff.float().cpu(), 1, top)
@@ -589,6 +596,41 @@ def test_expert_seams_match_block(dev, experts, router_w, T):
     # the block runs other kernels (the decode block at T <= 8): the layer bar
     assert_close_layer(sel.float().cpu(), ref_blk.cpu(), "selective-loading seam vs block", 2e-2, 5e-3)
     assert_close_layer(bw.float().cpu(), ref_blk.cpu(), "blockwise seam vs block", 2e-2, 5e-3)
+
+
+@pytest.mark.parametrize("T", [4, 96])
+def test_expert_seams_early_affinity_modulation(dev, experts, router_w, T):
+    """early_expert_affinity_modulation=True (qwen_with_nki.py:5768-5775,
+    3449): both seams scale each (token, expert) pair's input row by its
+    affinity and add the MLP outputs unscaled.  The scaled rows are rounded
+    to bf16 (the experts read bf16), so the bar against the fp32 oracle of
+    the same schedule is the layer bar, 2e-2 / 5e-3.  T = 4 runs the expert
+    GEMVs on 32 pair rows, T = 96 the grouped GEMMs on 768.  The late
+    (output-scaled) schedule is far from both: the flag took effect."""
+    announce(f"expert seams, early affinity modulation, T={T}")
+    w13, w2 = experts
+    g = torch.Generator(device=dev).manual_seed(4242 + T)
+    x = bf16_randn((T, H), g, dev)
+    blk = MoEBlock(router_w, w13, w2, K_TOP)
+    blk(x)
+    logits, tw, ti = blk.last_routing
+    ex = blk.experts
+    ex.routed_experts_mlp_config.early_expert_affinity_modulation = True
+    aff = torch.softmax(logits, dim=-1)
+    xf = x.float()
+    sel = ex.forward_selective_loading(xf, aff, ti)
+    bw = _blockwise_seam(ex, xf, ti, tw)
+    torch.cuda.synchronize()
+    top = ti.long().cpu()
+    chosen = torch.gather(aff.float().cpu(), 1, top)
+    w_sel = chosen / chosen.sum(dim=1, keepdim=True)
+    cache = _ExpertCache(w13, w2)
+    ref_sel = oracle.moe_experts_early(x.cpu(), top, w_sel, cache)
+    ref_bw = oracle.moe_experts_early(x.cpu(), top, tw.float().cpu(), cache)
+    assert_close_layer(sel.float().cpu(), ref_sel, "early selective-loading seam vs oracle", 2e-2, 5e-3)
+    assert_close_layer(bw.float().cpu(), ref_bw, "early blockwise seam vs oracle", 2e-2, 5e-3)
+    late = _oracle_rows(x.cpu(), top, tw.float().cpu(), cache, range(T))
+    assert max_abs(bw.float().cpu(), late) > 10 * max_abs(bw.float().cpu(), ref_bw)
 
 
 # --------------------------------------------------------------------------- attention

@@ -1,8 +1,8 @@
 """CPU tests of the model's host logic: the HF checkpoint converter (key
 mapping, layouts, lm_head / tied embeddings, fp8 block dequantisation, lazy
 safetensors shards), the attention-mask contract of the decoder layer, the
-KV-cache (K, V) pair contract, and the seams' rejection of the early affinity
-modulation schedule.  No GPU is touched.
+KV-cache (K, V) pair contract, and that the seams' early affinity modulation
+schedule has no CPU fallback.  No GPU is touched.
 """
 
 import pytest
@@ -221,15 +221,18 @@ def test_kv_cache_pair_contract():
     assert KVCache.wrap(c) is c
 
 
-def test_seams_reject_early_affinity_modulation():
-    """qwen_with_nki.py:5768-5775 (prefill) and 3449 (decode): the affinity
-    applied to the MLP input is another schedule; the seams refuse it."""
+def test_seams_early_affinity_modulation_has_no_cpu_fallback():
+    """qwen_with_nki.py:5768-5775 (prefill) and 3449 (decode): the flag is off
+    by default (Qwen3's setting); set, both seams take the early schedule,
+    which runs on the HIP kernels only and so refuses host tensors."""
     ex = ExpertMLPs(torch.zeros(4, 64, 512, dtype=torch.bfloat16), torch.zeros(4, 4, 512, 8, dtype=torch.bfloat16), 2)
     assert ex.routed_experts_mlp_config.early_expert_affinity_modulation is False
     ex.routed_experts_mlp_config.early_expert_affinity_modulation = True
     x = torch.zeros(3, 512)
-    with pytest.raises(ValueError, match="early_expert_affinity_modulation"):
-        ex.torch_blockwise_matmul_inference(4, 2, x, torch.zeros(3, 4), torch.zeros(8, dtype=torch.long),
-                                            torch.zeros(2, dtype=torch.long))
-    with pytest.raises(ValueError, match="early_expert_affinity_modulation"):
+    masked = torch.zeros(3, 4)
+    masked[:, :2] = 0.5
+    tpid = torch.tensor([0, 1, 2, 3, 0, 1, 2, 3], dtype=torch.long)
+    with pytest.raises(ValueError, match="must be on a GPU"):
+        ex.torch_blockwise_matmul_inference(4, 2, x, masked, tpid, torch.tensor([0, 1], dtype=torch.long))
+    with pytest.raises(ValueError, match="must be on a GPU"):
         ex.forward_selective_loading(x, torch.zeros(3, 4), torch.zeros(3, 2, dtype=torch.long))

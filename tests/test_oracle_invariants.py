@@ -151,6 +151,57 @@ def test_moe_block_k1_single_expert_is_dense_swiglu():
     np.testing.assert_allclose(out.numpy(), dense.numpy(), rtol=1e-5, atol=1e-5)
 
 
+def _early_case(seed, T=6, E=5, H=16, I=8, k=2):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g)
+    router = torch.randn(E, H, generator=g)
+    gate_up = 0.3 * torch.randn(E, H, 2 * I, generator=g)
+    down = 0.3 * torch.randn(E, I, H, generator=g)
+    return x, router, gate_up, down, {e: (gate_up[e], down[e]) for e in range(E)}
+
+
+def test_moe_experts_early_k1_is_the_late_block():
+    """k = 1: the renormalised affinity is 1, so scaling the input or the
+    output is the same; the result equals moe_block_prefill's."""
+    x, router, gate_up, down, experts = _early_case(5)
+    late, top_i, top_w, _ = oracle.moe_block_prefill(x, router, gate_up, down, 1)
+    assert torch.all(top_w == 1.0)
+    early = oracle.moe_experts_early(x, top_i, top_w, experts)
+    np.testing.assert_allclose(early.numpy(), late.numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_moe_experts_early_small_affinity_limit():
+    """silu(z) = z / 2 + O(z^2): with every affinity a -> 0 the early output
+    over a^2 tends to 0.5 * sum_j ((x Wg_j) * (x Wu_j)) Wd_j.  An affinity
+    applied to the output instead would scale as a (ratio -> infinity), one
+    read from the wrong pair would change the sum."""
+    x, router, gate_up, down, experts = _early_case(9, k=3)
+    _, top_i, _, _ = oracle.moe_block_prefill(x, router, gate_up, down, 3)
+    I = down.shape[1]
+    xd = x.double()
+    limit = torch.zeros(x.shape, dtype=torch.float64)
+    for t in range(x.shape[0]):
+        for e in top_i[t].tolist():
+            gu = xd[t] @ gate_up[e].double()
+            limit[t] += 0.5 * (gu[:I] * gu[I:]) @ down[e].double()
+    for a in (1e-2, 1e-3):
+        out = oracle.moe_experts_early(x, top_i, torch.full(top_i.shape, a), experts).double() / a**2
+        err = (out - limit).abs().max().item() / limit.abs().max().item()
+        assert err < 30 * a, (a, err)
+
+
+def test_moe_experts_early_is_a_sum_over_pairs():
+    """The k pairs of a token are independent: the output is the sum of k
+    one-pair calls, each with its own affinity."""
+    x, router, gate_up, down, experts = _early_case(13, k=2)
+    _, top_i, top_w, _ = oracle.moe_block_prefill(x, router, gate_up, down, 2)
+    full = oracle.moe_experts_early(x, top_i, top_w, experts)
+    parts = sum(oracle.moe_experts_early(x, top_i[:, j : j + 1], top_w[:, j : j + 1], experts) for j in range(2))
+    np.testing.assert_allclose(full.numpy(), parts.numpy(), rtol=1e-5, atol=1e-6)
+    late = oracle.moe_block_prefill(x, router, gate_up, down, 2)[0]
+    assert (full - late).abs().max() > 1e-2  # a different schedule, not the late one
+
+
 def test_pack_w13_interleave():
     E, H, I = 2, 4, 64
     gate_up = torch.arange(E * H * 2 * I, dtype=torch.float32).view(E, H, 2 * I)
