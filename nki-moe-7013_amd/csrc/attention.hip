@@ -1164,20 +1164,25 @@ __global__ __launch_bounds__(HD) void attn_decode_merge_kernel(const float* __re
   __shared__ float sred[2];
   const int bh = blockIdx.x;  // b * Hq + h
   const int d = threadIdx.x, lane = d & 63, wave = d >> 6;
+  const float* p = partial + int64_t(bh) * nsplit * AD_PSTR;
+  // Loads that wait for nothing go out first, together with the context
+  // length: this thread's (m, l) of partial min(d, nsplit - 1) and the first
+  // AD_MERGE_PF o values of its dim.  Every index stays below nsplit (the
+  // row's records); values of partials past the visible ones are dropped by
+  // the selects below and never enter arithmetic.
+  const int dr = min(d, nsplit - 1);
+  const float m_raw = p[int64_t(dr) * AD_PSTR];
+  const float l_raw = p[int64_t(dr) * AD_PSTR + 1];
+  float ov[AD_MERGE_PF];
+#pragma unroll
+  for (int u = 0; u < AD_MERGE_PF; ++u) ov[u] = p[int64_t(min(u, nsplit - 1)) * AD_PSTR + 4 + d];
   const int ctx = max_pos > 0 ? ad_ctx_pos(ctx_len, bh / Hq, S_max, max_pos, max_ctx)
                               : ad_ctx(ctx_len, chunk_start, bh / Hq, qpb, S_max, max_ctx);
   const int live = min(nsplit, (ctx + split_keys - 1) / split_keys);
-  const float* p = partial + int64_t(bh) * nsplit * AD_PSTR;
-  // Loads that do not depend on the running max go out first: this thread's
-  // (m, l) of partial d and the first AD_MERGE_PF o values of its dim.
-  float mv = -INFINITY, lv = 0.0f;
-  if (d < live) {
-    mv = p[int64_t(d) * AD_PSTR];
-    lv = p[int64_t(d) * AD_PSTR + 1];
-  }
-  float ov[AD_MERGE_PF];
+  const float mv = d < live ? m_raw : -INFINITY;
+  const float lv = d < live ? l_raw : 0.0f;
 #pragma unroll
-  for (int u = 0; u < AD_MERGE_PF; ++u) ov[u] = u < live ? p[int64_t(u) * AD_PSTR + 4 + d] : 0.0f;
+  for (int u = 0; u < AD_MERGE_PF; ++u) ov[u] = u < live ? ov[u] : 0.0f;
   float mloc = mv;
   for (int s = d + HD; s < live; s += HD) mloc = fmaxf(mloc, p[int64_t(s) * AD_PSTR]);
   mloc = wave_max(mloc);
