@@ -926,7 +926,7 @@ def cpu_baseline(layer, attn_gpu, lm_head_gpu, prefill_case, dev, seconds):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+        print(f"bench.py: measures one GPU; --gpus {a.gpus} is not supported "
               "(multi-GPU sharding is design-only)", file=sys.stderr)
         sys.exit(2)
     if a.traffic_probe:

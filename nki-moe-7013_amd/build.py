@@ -88,8 +88,8 @@ def build(jobs: int = 8) -> str:
 
 
 def _write_build_info() -> None:
-    """Record the commit the library was built from next to it (the GPU box
-    runs a copy of the tree without .git, so bench.py reads this file)."""
+    """Record the commit the library was built from next to it (a copy of
+    the tree without .git can still name its commit: bench.py reads this file)."""
     def git(*args):
         try:
             return subprocess.run(["git", *args], cwd=ROOT, capture_output=True, text=True,

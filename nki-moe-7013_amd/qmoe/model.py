@@ -55,11 +55,11 @@ class MoENeuronConfig:
         if isinstance(dt, str):
             dt = getattr(torch, dt.replace("torch.", ""))
         if dt != torch.bfloat16:
-            raise ValueError("this build computes in bfloat16 (torch_dtype must be bfloat16)")
+            raise ValueError("qmoe computes in bfloat16 (torch_dtype must be bfloat16)")
         self.torch_dtype = dt
         self.tp_degree = int(kwargs.pop("tp_degree", 1))
         if self.tp_degree != 1:
-            raise ValueError("this build runs on one GPU: tp_degree must be 1")
+            raise ValueError("qmoe runs on one GPU: tp_degree must be 1")
         self.on_device_sampling_config = kwargs.pop("on_device_sampling_config", None)
         self.enable_fused_speculation = False
         # prompt-lookup speculation: candidates + 1 tokens verified per step
@@ -424,7 +424,7 @@ class SafetensorsDir(Mapping):
 
 def convert_qwen3_moe_hf_to_neuron_state_dict(state_dict, config: Qwen3MoeInferenceConfig,
                                                device=None) -> Dict[str, Any]:
-    """HF checkpoint tensors -> this build's parameter tree.
+    """HF checkpoint tensors -> the qmoe parameter tree.
 
     Same key mapping as convert_qwen3_moe_hf_to_neuron_state_dict
     (qwen_with_nki.py:8883-8997): fp8 block dequantisation of every weight

@@ -1,7 +1,7 @@
 """fp32 reference of the Qwen3-MoE model, built from the oracle's functions.
 
 Runs on whatever device the weights live on (the oracle's torch code is
-device-agnostic), so the 48-layer model can be checked on the GPU box.  It
+device-agnostic), so the 48-layer model can be checked on the GPU.  It
 reads the same bf16 weights as the product (upcast exactly to fp32) and
 keeps every activation in fp32.
 """
